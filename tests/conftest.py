@@ -1,0 +1,43 @@
+import os
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+sys.path.insert(0, str(ROOT))
+sys.path.insert(0, str(Path(__file__).resolve().parent))
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950); runs through the C ABI on the device")
+    config.addinivalue_line("markers", "ref: needs the reference build in oracle/_ref (this container only)")
+
+
+def _has_gpu() -> bool:
+    # Counting devices does not initialise HIP in this image's runtime; the library's own
+    # device check runs inside the tests.
+    return os.path.exists("/dev/kfd")
+
+
+@pytest.fixture(scope="session")
+def uk():
+    import unikern_amd
+
+    return unikern_amd
+
+
+@pytest.fixture(scope="session")
+def gpu(uk):
+    arch = uk.device_check()
+    assert arch.startswith("gfx950"), arch
+    return uk
+
+
+@pytest.fixture(scope="session")
+def ref():
+    import _oracle
+
+    if not _oracle.ref_available():
+        pytest.skip("oracle/_ref/libukref.so not built (needs the reference tree; never on the GPU box)")
+    return _oracle.ref()

@@ -1,0 +1,162 @@
+"""Parity of the row family (row-sum, RMSNorm, softmax), standalone channelscale and the 1-D
+reduce on the MI355X against the CPU oracle, through the C ABI.
+
+Gates (stated here, from the north star): row-sum |y - r| <= 1e-5 * sum|x| per row;
+RMSNorm and softmax max |y - r| / max(|r|, 1e-6) <= 1e-5 (the reference's metric,
+src/codegen_hip.cpp:1410-1416, at the north-star tolerance); channelscale bit-exact (one
+correctly rounded multiply); sawtooth ("exact mode") row sums bit-exact.
+"""
+import numpy as np
+import pytest
+
+import _oracle as O
+
+pytestmark = pytest.mark.gpu
+
+ROWS_VARIANTS = [(64, 1), (64, 2), (64, 4), (64, 8), (64, 16), (128, 4), (128, 8), (256, 1), (256, 2), (256, 4),
+                 (256, 8), (512, 2), (512, 4), (1024, 1), (1024, 2), (1024, 4)]
+
+
+def run_op(uk, op, X, W=None, plan=None, eps=1e-6):
+    L, C = X.shape
+    d = uk.make_desc(op, [L, C], eps=eps)
+    xb = uk.DeviceBuffer.from_array(X)
+    ins = [xb]
+    if W is not None:
+        ins.append(uk.DeviceBuffer.from_array(W))
+    out_shape = (L,) if op == "reduce" else (L, C)
+    yb = uk.DeviceBuffer(int(np.prod(out_shape)) * 4)
+    yb.fill(0xFF)  # NaN pattern: an output the kernel does not write fails the comparison
+    uk.launch(d, ins, yb, plan=plan)
+    return yb.download(np.float32, out_shape)
+
+
+def rows_plan(uk, variant):
+    p = uk.Plan()
+    p.family = 1
+    p.variant = variant
+    return p
+
+
+def check_rowsum(X, Y):
+    r, a = O.rowsum_f64(X)
+    ref_order = O.rowsum_blocked(X)  # the reference's own basis (width 1024)
+    assert np.all(np.abs(Y.astype(np.float64) - r) <= 1e-5 * a), "row-sum gate vs binary64"
+    assert np.all(np.abs(Y.astype(np.float64) - ref_order.astype(np.float64)) <= 1e-5 * a), "vs reference order"
+
+
+def max_rel(y, r):
+    r64 = r.astype(np.float64)
+    return float(np.max(np.abs(y.astype(np.float64) - r64) / np.maximum(np.abs(r64), 1e-6)))
+
+
+SHAPES = [(4096, 4096), (64, 256), (3, 4096), (1, 4), (7, 1000), (2, 16384), (130, 512), (65536, 256)]
+
+
+@pytest.mark.parametrize("L,C", SHAPES)
+def test_rowsum_solver_plan(gpu, L, C):
+    X = O.normal(L * C, 20261201 + 10 + L + C, 0.0, 1.0).reshape(L, C)
+    check_rowsum(X, run_op(gpu, "reduce", X))
+
+
+@pytest.mark.parametrize("L,C", SHAPES)
+def test_rmsnorm_solver_plan(gpu, L, C):
+    X = O.normal(L * C, 20261201 + 10 + L, 0.0, 1.0).reshape(L, C)
+    W = O.normal(C, 20261201 + 11, 1.0, 0.1)
+    Y = run_op(gpu, "rmsnorm", X, W)
+    assert max_rel(Y, O.rmsnorm(X, W)) <= 1e-5
+
+
+@pytest.mark.parametrize("L,C", SHAPES)
+def test_softmax_solver_plan(gpu, L, C):
+    X = O.normal(L * C, 20261201 + 12 + L, 0.0, 8.0).reshape(L, C)
+    Y = run_op(gpu, "softmax", X)
+    assert max_rel(Y, O.softmax(X)) <= 1e-5
+    assert np.allclose(Y.astype(np.float64).sum(axis=1), 1.0, atol=1e-4)
+
+
+@pytest.mark.parametrize("vi", range(len(ROWS_VARIANTS)))
+def test_every_rows_variant(gpu, vi):
+    tpr, nv = ROWS_VARIANTS[vi]
+    cap = tpr * nv * 4
+    for C in sorted({cap, max(4, cap // 2 + 4), max(4, cap - 4)}):
+        L = 37
+        X = O.normal(L * C, 7 + C, 0.0, 2.0).reshape(L, C)
+        W = O.normal(C, 8 + C, 1.0, 0.1)
+        plan = rows_plan(gpu, vi)
+        check_rowsum(X, run_op(gpu, "reduce", X, plan=plan))
+        assert max_rel(run_op(gpu, "rmsnorm", X, W, plan=plan), O.rmsnorm(X, W)) <= 1e-5
+        assert max_rel(run_op(gpu, "softmax", X * 4, plan=plan), O.softmax(X * 4)) <= 1e-5
+
+
+@pytest.mark.parametrize("L,C", [(5, 1001), (3, 3), (2, 70001), (1, 1)])
+def test_stream_fallback_any_length(gpu, L, C):
+    sol = gpu.solve(gpu.make_desc("softmax", [L, C]))
+    assert sol.family == "rows_stream"
+    X = O.normal(L * C, 99 + C, 0.0, 3.0).reshape(L, C)
+    W = O.normal(C, 98 + C, 1.0, 0.1)
+    check_rowsum(X, run_op(gpu, "reduce", X))
+    assert max_rel(run_op(gpu, "rmsnorm", X, W), O.rmsnorm(X, W)) <= 1e-5
+    assert max_rel(run_op(gpu, "softmax", X), O.softmax(X)) <= 1e-5
+
+
+def test_rowsum_exact_mode_bit_exact(gpu):
+    # Sawtooth rows in 2^-4 units (the reference's initX): every partial sum is exact, so the
+    # GPU must equal the reference-order CPU sum bit for bit.
+    L, C = 1024, 4096
+    X = O.sawtooth(L * C, 17, 8).reshape(L, C)
+    Y = run_op(gpu, "reduce", X)
+    assert np.array_equal(Y.view(np.uint32), O.rowsum_blocked(X).view(np.uint32))
+
+
+def test_constant_rows_closed_forms(gpu):
+    # softmax of a constant row is 1/C exactly; rmsnorm of a constant row v with unit gain is
+    # v / sqrt(v^2 + eps) (one rounding each for the divide, sqrt and multiplies).
+    L, C = 8, 4096
+    X = np.full((L, C), 0.75, np.float32)
+    Y = run_op(gpu, "softmax", X)
+    assert np.all(Y == np.float32(1.0 / C))
+    W = np.ones(C, np.float32)
+    Yr = run_op(gpu, "rmsnorm", X, W)
+    assert np.array_equal(Yr, O.rmsnorm(X, W))
+
+
+def test_softmax_large_magnitudes_need_max_subtraction(gpu):
+    # exp(x) overflows binary32 above 88.7: without max subtraction these rows become inf/nan.
+    L, C = 16, 2048
+    X = O.normal(L * C, 5, 0.0, 40.0).reshape(L, C) + 100.0
+    Y = run_op(gpu, "softmax", X)
+    assert np.all(np.isfinite(Y))
+    assert max_rel(Y, O.softmax(X)) <= 1e-5
+
+
+@pytest.mark.parametrize("L,C", [(4096, 4096), (65536, 256), (3, 7), (1, 1), (5, 12)])
+def test_channelscale_bit_exact(gpu, L, C):
+    X = O.normal(L * C, 31 + C, 0.0, 1.0).reshape(L, C)
+    S = O.uniform(C, 32, 0.5, 1.5)
+    Y = run_op(gpu, "channelscale", X, S)
+    assert np.array_equal(Y.view(np.uint32), O.channelscale(X, S).view(np.uint32))
+
+
+@pytest.mark.parametrize("n", [1, 3, 1000, 1 << 20, 4194304, 12345679])
+def test_reduce1d(gpu, n):
+    x = O.normal(n, 40 + n, 0.0, 1.0)
+    d = gpu.make_desc("reduce", [n])
+    xb = gpu.DeviceBuffer.from_array(x)
+    yb = gpu.DeviceBuffer(4)
+    gpu.launch(d, [xb], yb)
+    y = float(yb.download(np.float32, (1,))[0])
+    exact = float(np.sum(x.astype(np.float64)))
+    assert abs(y - exact) <= 1e-5 * float(np.sum(np.abs(x.astype(np.float64))))
+    assert abs(y - float(O.reduce_blocked(x))) <= 1e-5 * float(np.sum(np.abs(x.astype(np.float64))))
+
+
+def test_reduce1d_reference_verify_instance(gpu):
+    # The reference's own device verify (src/codegen_hip.cpp:916-941): 2^20 values of 2^-6 sum to
+    # exactly 16384 in any binary32 order.
+    x = np.full(1 << 20, 0.015625, np.float32)
+    d = gpu.make_desc("reduce", [x.size])
+    xb = gpu.DeviceBuffer.from_array(x)
+    yb = gpu.DeviceBuffer(4)
+    gpu.launch(d, [xb], yb)
+    assert yb.download(np.float32, (1,))[0] == np.float32(16384.0)

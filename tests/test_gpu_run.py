@@ -1,0 +1,60 @@
+"""uk_run end to end (the emitted-program contract: seeded inputs, verified launch, timing,
+UNIKERN_RESULT line) on the BASELINE configurations, through the C ABI."""
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def _ok(r):
+    assert r.exit_code == 0, r.log
+    assert r.built and r.ran and r.verified, r.log
+    assert r.migrations == 0 and r.checks > 0
+    assert r.kernel_ms > 0 and r.measured_ms >= r.kernel_ms
+    assert r.line.startswith("UNIKERN_RESULT backend=amd verify=PASS")
+
+
+@pytest.mark.parametrize("op", ["reduce", "rmsnorm", "softmax"])
+def test_run_reduction_family_config(gpu, op):
+    r = gpu.run(gpu.make_desc(op, [4096, 4096]), iters=20)
+    _ok(r)
+    assert r.bound == "hbm" and r.peak == 8000.0
+    print(r.line)
+
+
+@pytest.mark.parametrize("op", ["reduce", "rmsnorm", "softmax", "channelscale"])
+def test_run_reference_sample_shapes_exact_mode(gpu, op):
+    # samples/kml_{softmax,rmsnorm,channelscale}.json shape, the reference's sawtooth inputs.
+    r = gpu.run(gpu.make_desc(op, [65536, 256]), exact=True, iters=10)
+    _ok(r)
+
+
+def test_run_gemm_f16_config(gpu):
+    r = gpu.run(gpu.make_desc("gemm", [4096, 4096, 4096], dtype="fp16", layout="TN"), iters=10)
+    _ok(r)
+    assert r.bound == "mfma" and r.err_metric <= 1e-2
+    print(r.line)
+
+
+def test_run_gemm_f16_exact_mode_bit_exact(gpu):
+    r = gpu.run(gpu.make_desc("gemm", [1024, 1024, 1024], dtype="fp16", layout="TN"), exact=True, iters=5)
+    _ok(r)
+    assert r.err_metric == 0  # bit-exact mismatches
+
+
+def test_run_reference_gemm_samples(gpu):
+    # samples/kml_gemm.json (fp32 512^3 NT) and kml_gemm_f16.json (fp16 512^3 NT), exact mode.
+    for dt in ("fp32", "fp16"):
+        r = gpu.run(gpu.make_desc("gemm", [512, 512, 512], dtype=dt), exact=True, iters=5)
+        _ok(r)
+        assert r.err_metric == 0
+
+
+def test_run_reduce1d_sample(gpu):
+    r = gpu.run(gpu.make_desc("reduce", [4194304]), iters=20)
+    _ok(r)
+
+
+def test_run_refuses_unsupported(gpu):
+    r = gpu.run(gpu.make_desc("softmax", [16, 16], dtype="fp16"))
+    assert r.exit_code == 2 and not r.ran
+    assert "op_unsupported" in r.log

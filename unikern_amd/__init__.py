@@ -1,0 +1,287 @@
+"""unikern_amd — UNIKERN's kernel hot path, native to one MI355X (gfx950).
+
+Python face of libunikern_hip.so (include/unikern_hip.h). It mirrors the reference's C++
+interface for the path (include/unikern/components.hpp, include/unikern/codegen.hpp):
+
+    kml_import / kml_export / canonical_form / op_signature / workload_of   (src/kml_front.cpp, src/kml.cpp)
+    hcs_fingerprint / hcs_export                                           (src/hcs.cpp)
+    solve                                                                  (src/solver.cpp)
+    run -> RunOutcome                                                      (run_hip, src/runner.cpp:146-238)
+    launch                                                                 (raw operator on device buffers)
+
+There is no CPU fallback: importing fails when the library is missing, and every execution
+entry point runs the HIP kernels.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+from pathlib import Path
+
+import numpy as np
+
+from . import _capi
+from ._capi import (DTYPES, FAMILIES, LAYOUTS, OPS, UK_BAD_INVOCATION, UK_HIP_FAILURE, UK_INFEASIBLE, UK_OK,
+                    UK_RESIDENCY, UK_VERIFY_FAIL, OpDesc, Plan, Result)
+
+lib = _capi.load()
+
+SEED = 20261201
+ROOT = Path(__file__).resolve().parent.parent
+SAMPLES = ROOT / "samples"
+
+
+class KmlError(ValueError):
+    """A rejected KML declaration; the message lists every violation."""
+
+
+class UnikernError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+def last_error() -> str:
+    e = lib.uk_last_error()
+    return e.decode() if e else ""
+
+
+def _buf(n: int = 1 << 16):
+    return C.create_string_buffer(n)
+
+
+def _text(json_text: str | bytes) -> bytes:
+    return json_text.encode() if isinstance(json_text, str) else json_text
+
+
+# ---------------------------------------------------------------------------------------
+# KML front end
+# ---------------------------------------------------------------------------------------
+def kml_import(text: str) -> OpDesc:
+    d = OpDesc()
+    err = _buf()
+    rc = lib.uk_kml_import(_text(text), C.byref(d), err, len(err))
+    if rc != UK_OK:
+        raise KmlError(err.value.decode())
+    return d
+
+
+def kml_load(path: str | Path) -> OpDesc:
+    return kml_import(Path(path).read_text())
+
+
+def _str_call(fn, text) -> str:
+    out = _buf()
+    n = fn(_text(text), out, len(out))
+    if n < 0:
+        raise KmlError(last_error())
+    return out.value.decode()
+
+
+def kml_export(text: str) -> str:
+    return _str_call(lib.uk_kml_export, text)
+
+
+def canonical_form(text: str) -> str:
+    return _str_call(lib.uk_kml_canonical, text)
+
+
+def tree_hash(text: str) -> str:
+    return _str_call(lib.uk_kml_tree_hash, text)
+
+
+def op_signature(d: OpDesc) -> str:
+    out = _buf(256)
+    if lib.uk_op_signature(C.byref(d), out, len(out)) < 0:
+        raise KmlError(last_error())
+    return out.value.decode()
+
+
+def workload_of(d: OpDesc) -> dict:
+    ops, nbytes, wbytes = C.c_int64(), C.c_int64(), C.c_int64()
+    rc = lib.uk_workload(C.byref(d), C.byref(ops), C.byref(nbytes), C.byref(wbytes))
+    if rc != UK_OK:
+        raise KmlError(last_error())
+    return {"ops": ops.value, "bytes": nbytes.value, "weight_bytes": wbytes.value}
+
+
+def support_gap(d: OpDesc) -> str:
+    out = _buf(1024)
+    lib.uk_support_gap(C.byref(d), out, len(out))
+    return out.value.decode()
+
+
+def make_desc(op: str, dims, dtype: str = "fp32", layout: str = "NT", *, batch: int = 1, pad: int = 0,
+              stride: int = 1, epilogue: str = "none", eps: float = 1e-6, tile_m: int = 64,
+              tile_n: int = 128) -> OpDesc:
+    """Build a descriptor directly (same meaning as a KML declaration)."""
+    d = OpDesc()
+    d.op, d.dtype, d.layout = OPS[op], DTYPES[dtype], LAYOUTS[layout]
+    d.epilogue = 1 if epilogue == "channelscale" else 0
+    d.ndims = len(dims)
+    for i, v in enumerate(dims):
+        d.dims[i] = int(v)
+    d.tile_m, d.tile_n = tile_m, tile_n
+    d.batch, d.pad, d.stride, d.eps = batch, pad, stride, eps
+    return d
+
+
+# ---------------------------------------------------------------------------------------
+# HCS + solver
+# ---------------------------------------------------------------------------------------
+def hcs_fingerprint(hcs_json: str | None = None) -> str:
+    out = _buf(256)
+    rc = lib.uk_hcs_fingerprint(None if hcs_json is None else _text(hcs_json), out, len(out))
+    if rc != UK_OK:
+        raise ValueError(out.value.decode())
+    return out.value.decode()
+
+
+def hcs_export(hcs_json: str | None = None) -> str:
+    out = _buf()
+    n = lib.uk_hcs_export(None if hcs_json is None else _text(hcs_json), out, len(out))
+    if n < 0:
+        raise ValueError(last_error())
+    return out.value.decode()
+
+
+@dataclass
+class Solution:
+    plan: Plan
+    family: str
+    key: str
+    predicted_us: float
+    feasible: int
+    log: str
+
+
+def solve(d: OpDesc, hcs_json: str | None = None) -> Solution:
+    p = Plan()
+    log = _buf()
+    rc = lib.uk_solve(None if hcs_json is None else _text(hcs_json), C.byref(d), C.byref(p), log, len(log))
+    if rc != UK_OK:
+        raise UnikernError(rc, log.value.decode() or last_error())
+    return Solution(p, FAMILIES.get(p.family, "?"), p.key.decode(), p.predicted_us, p.feasible, log.value.decode())
+
+
+# ---------------------------------------------------------------------------------------
+# Execution
+# ---------------------------------------------------------------------------------------
+@dataclass
+class RunOutcome:
+    """Mirror of the reference's RunOutcome (include/unikern/codegen.hpp:49-83) plus roofline."""
+    built: bool
+    ran: bool
+    verified: bool
+    exit_code: int
+    max_rel: float
+    err_metric: float
+    tol: float
+    kernel_ms: float
+    measured_ms: float
+    achieved: float
+    peak: float
+    frac: float
+    bound: str
+    migrations: int
+    checks: int
+    vram_free: int
+    vram_total: int
+    plan_key: str
+    family: str
+    sets: int
+    log: str
+    line: str
+    raw: Result = field(repr=False, default=None)
+
+
+def run(d: OpDesc, *, seed: int = SEED, exact: bool = False, iters: int = 50, plan: Plan | None = None,
+        hcs_json: str | None = None) -> RunOutcome:
+    r = Result()
+    log = _buf(1 << 16)
+    rc = lib.uk_run(None if hcs_json is None else _text(hcs_json), C.byref(d),
+                    None if plan is None else C.byref(plan), seed, 1 if exact else 0, iters, C.byref(r), log,
+                    len(log))
+    line = _buf(2048)
+    lib.uk_format_result(C.byref(r), line, len(line))
+    return RunOutcome(bool(r.built), bool(r.ran), bool(r.verified), rc, r.max_rel, r.err_metric, r.tol, r.kernel_ms,
+                      r.measured_ms, r.achieved, r.peak, r.frac, "mfma" if r.bound == 1 else "hbm", r.migrations,
+                      r.checks, r.vram_free, r.vram_total, r.plan.key.decode(), FAMILIES.get(r.plan.family, "?"),
+                      r.sets, log.value.decode(), line.value.decode(), r)
+
+
+def device_check() -> str:
+    arch = _buf(128)
+    rc = lib.uk_device_check(arch, len(arch))
+    if rc != UK_OK:
+        raise UnikernError(rc, last_error())
+    return arch.value.decode()
+
+
+def device_props() -> dict:
+    cus, lds, clk = C.c_int32(), C.c_int32(), C.c_int32()
+    tot = C.c_uint64()
+    rc = lib.uk_device_props(C.byref(cus), C.byref(lds), C.byref(clk), C.byref(tot))
+    if rc != UK_OK:
+        raise UnikernError(rc, last_error())
+    return {"compute_units": cus.value, "lds_per_block": lds.value, "clock_khz": clk.value,
+            "total_bytes": tot.value}
+
+
+def _check(rc: int):
+    if rc != UK_OK:
+        raise UnikernError(rc, last_error())
+
+
+class DeviceBuffer:
+    """Device allocation owned by Python; copies to/from numpy arrays."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = C.c_void_p()
+        _check(lib.uk_malloc(C.byref(p), self.nbytes))
+        self.ptr = p
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    def upload(self, a: np.ndarray):
+        a = np.ascontiguousarray(a)
+        assert a.nbytes <= self.nbytes
+        _check(lib.uk_memcpy_htod(self.ptr, a.ctypes.data_as(C.c_void_p), a.nbytes))
+
+    def download(self, dtype, shape) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        assert out.nbytes <= self.nbytes
+        _check(lib.uk_memcpy_dtoh(out.ctypes.data_as(C.c_void_p), self.ptr, out.nbytes))
+        return out
+
+    def fill(self, value: int):
+        _check(lib.uk_memset(self.ptr, value, self.nbytes))
+
+    def free(self):
+        if self.ptr:
+            lib.uk_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def launch(d: OpDesc, ins, out: DeviceBuffer, plan: Plan | None = None, stream=None, sync: bool = True):
+    arr = (C.c_void_p * len(ins))(*[b.ptr for b in ins])
+    rc = lib.uk_launch(C.byref(d), None if plan is None else C.byref(plan), arr, len(ins), out.ptr, stream)
+    _check(rc)
+    if sync:
+        _check(lib.uk_synchronize())
+
+
+def synchronize():
+    _check(lib.uk_synchronize())

@@ -1,0 +1,311 @@
+// GEMM on gfx950 matrix cores.
+//
+// Replaces the reference's SIMT uk_gemm / uk_gemm_h (src/codegen_hip.cpp:1089-1120,
+// :1777-1808), which convert to f32 in LDS and run scalar FMAs. Two kernels:
+//
+// gemm_f16_tn_kernel — the hot path: C[M][N] f16 = A[M][K] f16 . B^T, B stored [N][K]
+//   (column-major B: both operands K-contiguous), f32 accumulate in v_mfma_f32_32x32x16_f16.
+//   * BM x BN x BK macro tile per workgroup, WM x WN wavefronts, each a (BM/WM) x (BN/WN)
+//     block of 32x32 MFMA tiles with accumulators resident in AGPR/VGPR.
+//   * global -> LDS with global_load_lds_dwordx4 (no VGPR staging): one instruction moves
+//     8 rows x 128 B into 1 KiB of LDS; the 16-byte chunk index is XOR-swizzled by row on the
+//     global side, so the MFMA fragment reads (ds_read_b128, 32 rows at one k offset) hit
+//     distinct banks.
+//   * STAGES-deep LDS ring (2 x 64 KiB for 256x256x64), one barrier per k-tile.
+//   * workgroup -> tile mapping is XCD-aware: workgroup i runs on XCD i % 8, so ids are
+//     regrouped so each XCD owns a compact block of tiles and shares A/B panels in its L2.
+//   * the MFMA computes C^T tiles (B fragment as the first operand), so each lane holds four
+//     consecutive output columns per row; the epilogue converts to f16 (round to nearest
+//     even), stages the tile in LDS and writes rows with 128-bit stores.
+//
+// gemm_generic_kernel — any M, N, K, either B layout, f16 or f32 inputs: 64x64 tiles,
+//   bounds-checked element loads, MFMA 32x32x16 f16 or 32x32x2 f32. Used for shapes the
+//   fast kernel's divisibility predicates reject and for the f32 GEMM.
+#include "../launch.hpp"
+#include "../variants.hpp"
+#include "common.hpp"
+
+namespace uk::kern {
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <int BM, int BN, int BK, int WM, int WN, int STAGES>
+struct GemmF16Cfg {
+  static constexpr int kWaves = WM * WN;
+  static constexpr int kThreads = kWaves * 64;
+  static constexpr int kWTM = BM / WM;  // wave tile rows (M)
+  static constexpr int kWTN = BN / WN;  // wave tile cols (N)
+  static constexpr int kFM = kWTM / 32;
+  static constexpr int kFN = kWTN / 32;
+  static constexpr int kRowBytes = BK * 2;
+  static constexpr int kChunks = kRowBytes / 16;  // 16-byte chunks per LDS row
+  static constexpr int kRowsPerInst = 1024 / kRowBytes;
+  static constexpr int kStageBytes = (BM + BN) * kRowBytes;
+  static constexpr int kPitch = kWTN * 2 + 16;  // epilogue staging row pitch (bytes)
+  static constexpr int kEpiBytes = kWaves * kWTM * kPitch;
+  static constexpr int kLdsBytes = (STAGES * kStageBytes > kEpiBytes) ? STAGES * kStageBytes : kEpiBytes;
+  static_assert(kWTM % 32 == 0 && kWTN % 32 == 0, "wave tile must be whole 32x32 MFMA tiles");
+  static_assert(BK % 16 == 0 && kChunks <= 8 && 1024 % kRowBytes == 0, "BK must be 16..64");
+  static_assert(BM % kRowsPerInst == 0 && BN % kRowsPerInst == 0, "tile rows per DMA instruction");
+};
+
+__device__ __forceinline__ int swz(int row, int chunks) { return (row & (chunks - 1)); }
+
+// Issue the DMA for a rows x BK tile starting at g (row pitch ld elements) into LDS dst.
+template <int ROWS, int BK, int WAVES>
+__device__ __forceinline__ void dma_tile(const _Float16* __restrict__ g, int64_t ld, char* dst, int wave, int lane) {
+  constexpr int kRowBytes = BK * 2;
+  constexpr int kChunks = kRowBytes / 16;
+  constexpr int kRowsPerInst = 1024 / kRowBytes;
+  constexpr int kInsts = ROWS / kRowsPerInst;
+  static_assert(kInsts % WAVES == 0, "DMA instructions must split evenly over the wavefronts");
+  const int rr = lane / kChunks;      // row within the instruction's row group
+  const int p = lane % kChunks;       // physical chunk this lane fills
+  const int w = __builtin_amdgcn_readfirstlane(wave);
+#pragma unroll
+  for (int t = 0; t < kInsts / WAVES; ++t) {
+    const int ins = t * WAVES + w;
+    const int r = ins * kRowsPerInst + rr;
+    const int c = p ^ swz(r, kChunks);  // logical chunk stored at physical chunk p
+    const _Float16* src = g + (int64_t)r * ld + c * 8;
+    __builtin_amdgcn_global_load_lds(src, (lds_void*)(dst + ins * 1024), 16, 0, 0);
+  }
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int STAGES>
+__global__ void __launch_bounds__(WM* WN * 64, 1)
+    gemm_f16_tn_kernel(const _Float16* __restrict__ A, const _Float16* __restrict__ B, _Float16* __restrict__ C,
+                       int M, int N, int K, int tiles_m, int tiles_n) {
+  using Cfg = GemmF16Cfg<BM, BN, BK, WM, WN, STAGES>;
+  __shared__ __attribute__((aligned(1024))) char lds[Cfg::kLdsBytes];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+
+  // XCD-aware tile mapping: make ids that share an XCD consecutive, then walk tiles in
+  // groups of 4 tile-rows so consecutive ids share A panels (rows) and B panels (columns).
+  const int G = gridDim.x;
+  int lin = blockIdx.x;
+  if ((G & 7) == 0) lin = (lin & 7) * (G >> 3) + (lin >> 3);
+  constexpr int kGroupM = 4;
+  const int per_group = kGroupM * tiles_n;
+  const int group = lin / per_group;
+  const int first_m = group * kGroupM;
+  const int gm = (tiles_m - first_m) < kGroupM ? (tiles_m - first_m) : kGroupM;
+  const int in_group = lin - group * per_group;
+  const int tm = first_m + in_group % gm;
+  const int tn = in_group / gm;
+
+  const int m0 = tm * BM, n0 = tn * BN;
+  const _Float16* Ag = A + (int64_t)m0 * K;
+  const _Float16* Bg = B + (int64_t)n0 * K;
+
+  const int wm = wave / WN, wn = wave % WN;
+  f32x16 acc[Cfg::kFM][Cfg::kFN];
+#pragma unroll
+  for (int i = 0; i < Cfg::kFM; ++i)
+#pragma unroll
+    for (int j = 0; j < Cfg::kFN; ++j) acc[i][j] = f32x16{};
+
+  const int KT = K / BK;
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s) {
+    if (s < KT) {
+      char* st = lds + s * Cfg::kStageBytes;
+      dma_tile<BM, BK, Cfg::kWaves>(Ag + s * BK, K, st, wave, lane);
+      dma_tile<BN, BK, Cfg::kWaves>(Bg + s * BK, K, st + BM * Cfg::kRowBytes, wave, lane);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  const int frow = lane & 31;      // fragment row within a 32-row MFMA tile
+  const int fchunk = lane >> 5;    // which 8-element half of the 16-wide k step
+  for (int kt = 0; kt < KT; ++kt) {
+    const int nxt = kt + STAGES - 1;
+    if (nxt < KT) {
+      char* st = lds + (nxt % STAGES) * Cfg::kStageBytes;
+      dma_tile<BM, BK, Cfg::kWaves>(Ag + nxt * BK, K, st, wave, lane);
+      dma_tile<BN, BK, Cfg::kWaves>(Bg + nxt * BK, K, st + BM * Cfg::kRowBytes, wave, lane);
+    }
+    const char* As = lds + (kt % STAGES) * Cfg::kStageBytes;
+    const char* Bs = As + BM * Cfg::kRowBytes;
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      const int c = kk * 2 + fchunk;
+      f16x8 a[Cfg::kFM], b[Cfg::kFN];
+#pragma unroll
+      for (int i = 0; i < Cfg::kFM; ++i) {
+        const int r = wm * Cfg::kWTM + i * 32 + frow;
+        a[i] = *reinterpret_cast<const f16x8*>(As + r * Cfg::kRowBytes + ((c ^ swz(r, Cfg::kChunks)) << 4));
+      }
+#pragma unroll
+      for (int j = 0; j < Cfg::kFN; ++j) {
+        const int r = wn * Cfg::kWTN + j * 32 + frow;
+        b[j] = *reinterpret_cast<const f16x8*>(Bs + r * Cfg::kRowBytes + ((c ^ swz(r, Cfg::kChunks)) << 4));
+      }
+#pragma unroll
+      for (int i = 0; i < Cfg::kFM; ++i)
+#pragma unroll
+        for (int j = 0; j < Cfg::kFN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[j], a[i], acc[i][j], 0, 0, 0);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
+
+  // Epilogue. acc[i][j] holds C^T: lane -> row m = i*32 + (lane & 31) of the wave tile and
+  // columns n = j*32 + 8*g + 4*(lane >> 5) + {0..3} for register group g = r / 4.
+  char* stage = lds + wave * (Cfg::kWTM * Cfg::kPitch);
+#pragma unroll
+  for (int i = 0; i < Cfg::kFM; ++i)
+#pragma unroll
+    for (int j = 0; j < Cfg::kFN; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        f16x4 h;
+        h[0] = (_Float16)acc[i][j][g * 4 + 0];
+        h[1] = (_Float16)acc[i][j][g * 4 + 1];
+        h[2] = (_Float16)acc[i][j][g * 4 + 2];
+        h[3] = (_Float16)acc[i][j][g * 4 + 3];
+        const int m = i * 32 + (lane & 31);
+        const int n = j * 32 + g * 8 + (lane >> 5) * 4;
+        *reinterpret_cast<f16x4*>(stage + m * Cfg::kPitch + n * 2) = h;
+      }
+  __syncthreads();
+  constexpr int kRowChunks = Cfg::kWTN * 2 / 16;
+  constexpr int kTotal = Cfg::kWTM * kRowChunks;
+  _Float16* Cw = C + (int64_t)(m0 + wm * Cfg::kWTM) * N + n0 + wn * Cfg::kWTN;
+#pragma unroll 4
+  for (int id = lane; id < kTotal; id += 64) {
+    const int r = id / kRowChunks, q = id % kRowChunks;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(stage + r * Cfg::kPitch + q * 16);
+    *reinterpret_cast<u32x4*>(Cw + (int64_t)r * N + q * 8) = v;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Generic MFMA GEMM: 64x64 tile, 4 wavefronts (2x2 of 32x32), BK = 16, bounds-checked.
+// T = _Float16 or float inputs; TO = output type; BT: B stored [N][K] (TN) else [K][N] (NT).
+// ---------------------------------------------------------------------------------------
+template <typename T, typename TO, bool BT>
+__global__ void __launch_bounds__(256)
+    gemm_generic_kernel(const T* __restrict__ A, const T* __restrict__ B, TO* __restrict__ C, int M, int N, int K) {
+  constexpr int BKg = 16;
+  __shared__ __attribute__((aligned(16))) T As[64][BKg];
+  __shared__ __attribute__((aligned(16))) T Bs[64][BKg];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+  const int wm = wave >> 1, wn = wave & 1;
+  f32x16 acc = f32x16{};
+  for (int k0 = 0; k0 < K; k0 += BKg) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int idx = tid * 4 + e;
+      const int r = idx / BKg, kk = idx % BKg;
+      const int gm = m0 + r, gk = k0 + kk;
+      As[r][kk] = (gm < M && gk < K) ? A[(int64_t)gm * K + gk] : T(0);
+      if (BT) {
+        const int gn = n0 + r;
+        Bs[r][kk] = (gn < N && gk < K) ? B[(int64_t)gn * K + gk] : T(0);
+      } else {
+        const int kr = idx / 64, nn = idx % 64;
+        const int gk2 = k0 + kr, gn = n0 + nn;
+        Bs[nn][kr] = (gn < N && gk2 < K) ? B[(int64_t)gk2 * N + gn] : T(0);
+      }
+    }
+    __syncthreads();
+    if constexpr (sizeof(T) == 2) {
+      const f16x8 a = *reinterpret_cast<const f16x8*>(&As[wm * 32 + (lane & 31)][(lane >> 5) * 8]);
+      const f16x8 b = *reinterpret_cast<const f16x8*>(&Bs[wn * 32 + (lane & 31)][(lane >> 5) * 8]);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc, 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int s = 0; s < BKg / 2; ++s) {
+        const float a = As[wm * 32 + (lane & 31)][2 * s + (lane >> 5)];
+        const float b = Bs[wn * 32 + (lane & 31)][2 * s + (lane >> 5)];
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc, 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+  // D[i][j]: lane -> column j = lane & 31, rows i = 8*(r/4) + 4*(lane>>5) + r%4.
+  const int n = n0 + wn * 32 + (lane & 31);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int m = m0 + wm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+    if (m < M && n < N) C[(int64_t)m * N + n] = (TO)acc[r];
+  }
+}
+
+}  // namespace uk::kern
+
+namespace uk {
+
+namespace {
+template <int I>
+hipError_t gemm_f16_variant(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, hipStream_t s) {
+  constexpr GemmF16Variant v = kGemmF16Variants[I];
+  using Cfg = kern::GemmF16Cfg<v.bm, v.bn, v.bk, v.wm, v.wn, v.stages>;
+  const int tiles_m = int(M / v.bm), tiles_n = int(N / v.bn);
+  hipLaunchKernelGGL((kern::gemm_f16_tn_kernel<v.bm, v.bn, v.bk, v.wm, v.wn, v.stages>),
+                     dim3((unsigned)(tiles_m * tiles_n)), dim3(Cfg::kThreads), 0, s,
+                     static_cast<const _Float16*>(A), static_cast<const _Float16*>(B), static_cast<_Float16*>(C),
+                     (int)M, (int)N, (int)K, tiles_m, tiles_n);
+  return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_gemm_f16(const Plan& p, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
+                           hipStream_t s) {
+  if (p.family != Family::GemmF16 || p.variant < 0 || p.variant >= kNumGemmF16Variants) return hipErrorInvalidValue;
+  const GemmF16Variant v = kGemmF16Variants[p.variant];
+  // The kernel has no bounds checks: every tile must be whole, and the DMA reads 16-byte
+  // chunks of K-contiguous rows.
+  if (M <= 0 || N <= 0 || K <= 0 || M % v.bm || N % v.bn || K % v.bk) return hipErrorInvalidValue;
+  if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX / 2) return hipErrorInvalidValue;
+  if ((((uintptr_t)A) | ((uintptr_t)B) | ((uintptr_t)C)) & 15) return hipErrorInvalidValue;
+  if ((M / v.bm) * (N / v.bn) > INT32_MAX) return hipErrorInvalidValue;
+  switch (p.variant) {
+    case 0: return gemm_f16_variant<0>(A, B, C, M, N, K, s);
+    case 1: return gemm_f16_variant<1>(A, B, C, M, N, K, s);
+    case 2: return gemm_f16_variant<2>(A, B, C, M, N, K, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_gemm_generic(DType dt, Layout lay, const void* A, const void* B, void* C, int64_t M, int64_t N,
+                               int64_t K, hipStream_t s) {
+  if (M <= 0 || N <= 0 || K <= 0 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return hipErrorInvalidValue;
+  if (lay != Layout::NT && lay != Layout::TN) return hipErrorInvalidValue;
+  if ((M + 63) / 64 > 65535) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
+  const bool bt = lay == Layout::TN;
+  if (dt == DType::F16) {
+    auto a = static_cast<const _Float16*>(A);
+    auto b = static_cast<const _Float16*>(B);
+    auto c = static_cast<_Float16*>(C);
+    if (bt)
+      hipLaunchKernelGGL((kern::gemm_generic_kernel<_Float16, _Float16, true>), grid, dim3(256), 0, s, a, b, c,
+                         (int)M, (int)N, (int)K);
+    else
+      hipLaunchKernelGGL((kern::gemm_generic_kernel<_Float16, _Float16, false>), grid, dim3(256), 0, s, a, b, c,
+                         (int)M, (int)N, (int)K);
+  } else if (dt == DType::F32) {
+    auto a = static_cast<const float*>(A);
+    auto b = static_cast<const float*>(B);
+    auto c = static_cast<float*>(C);
+    if (bt)
+      hipLaunchKernelGGL((kern::gemm_generic_kernel<float, float, true>), grid, dim3(256), 0, s, a, b, c, (int)M,
+                         (int)N, (int)K);
+    else
+      hipLaunchKernelGGL((kern::gemm_generic_kernel<float, float, false>), grid, dim3(256), 0, s, a, b, c, (int)M,
+                         (int)N, (int)K);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace uk

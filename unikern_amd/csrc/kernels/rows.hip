@@ -1,0 +1,367 @@
+// Row family on gfx950: row-sum, RMSNorm and softmax over X[L][C] f32.
+//
+// Replaces the reference's one-thread-per-row kernels (src/codegen_hip.cpp:1985-1996 softmax,
+// :2154-2164 rmsnorm) and its two-pass scalar reduce (:818-833, used here per row).
+// Design: tpr threads own one row; each thread keeps nv float4 of it in registers, loaded
+// with 128-bit coalesced loads (for a fixed register index the wavefront reads 1 KiB of
+// contiguous HBM). Reductions run inside the wavefront with DPP/swizzle/readlane; when a row
+// spans several wavefronts, one LDS slot per wavefront carries the partial and every thread
+// folds the slots in wavefront order (deterministic). X is read once and Y written once, so
+// the kernels are HBM-bound: algorithmic bytes are read(X) + write(Y) (+ W for RMSNorm).
+//
+// Semantics kept from the reference CPU loops: rmsnorm y = (x * rms) * W with
+// rms = 1/sqrt(sum(x^2)/C + eps) (correctly rounded divide and sqrt); softmax
+// y = exp(x - max) / sum(exp(x - max)) with an IEEE divide.
+#include <math.h>
+
+#include "../launch.hpp"
+#include "../variants.hpp"
+#include "common.hpp"
+
+namespace uk::kern {
+
+template <int TPR, int NV, int OP>
+__global__ void __launch_bounds__(TPR < 256 ? 256 : TPR)
+    rows_kernel(const float* __restrict__ X, const float* __restrict__ Wg, float* __restrict__ Y, int L, int C,
+                float eps) {
+  constexpr int WG = TPR < 256 ? 256 : TPR;
+  constexpr int RPW = WG / TPR;  // rows per workgroup
+  constexpr int WPR = TPR / 64;  // wavefronts per row
+  __shared__ float red0[WG / 64];
+  __shared__ float red1[WG / 64];
+
+  const int tid = threadIdx.x;
+  const int rloc = tid / TPR;
+  const int t = tid % TPR;
+  const int wave = tid >> 6;
+  const int64_t row = (int64_t)blockIdx.x * RPW + rloc;
+  const bool active = row < L;
+  const int C4 = C >> 2;
+  const f32x4* x4 = reinterpret_cast<const f32x4*>(X + (active ? row : 0) * (int64_t)C);
+
+  const float fill = (OP == 2) ? -INFINITY : 0.f;
+  f32x4 v[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int j = i * TPR + t;
+    if (active && j < C4) {
+      v[i] = x4[j];
+    } else {
+      v[i] = f32x4{fill, fill, fill, fill};
+    }
+  }
+
+  // Row reduction: wave-level, then (when the row spans wavefronts) an LDS fold in wave order.
+  auto row_reduce_sum = [&](float s, float* slots) -> float {
+    s = wave_sum(s);
+    if constexpr (WPR == 1) {
+      return s;
+    } else {
+      if ((tid & 63) == 0) slots[wave] = s;
+      __syncthreads();
+      float r = slots[rloc * WPR];
+#pragma unroll
+      for (int w = 1; w < WPR; ++w) r += slots[rloc * WPR + w];
+      return r;
+    }
+  };
+  auto row_reduce_max = [&](float m, float* slots) -> float {
+    m = wave_max(m);
+    if constexpr (WPR == 1) {
+      return m;
+    } else {
+      if ((tid & 63) == 0) slots[wave] = m;
+      __syncthreads();
+      float r = slots[rloc * WPR];
+#pragma unroll
+      for (int w = 1; w < WPR; ++w) r = fmaxf(r, slots[rloc * WPR + w]);
+      return r;
+    }
+  };
+
+  if constexpr (OP == 0) {  // row-sum
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    s = row_reduce_sum(s, red0);
+    if (active && t == 0) Y[row] = s;
+  } else if constexpr (OP == 1) {  // RMSNorm
+    const f32x4* w4 = reinterpret_cast<const f32x4*>(Wg);
+    f32x4 g[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int j = i * TPR + t;
+      g[i] = (j < C4) ? w4[j] : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      // __fmul_rn keeps the squares unfused from the adds, as in the reference CPU loop.
+      ss += (__fmul_rn(v[i].x, v[i].x) + __fmul_rn(v[i].y, v[i].y)) +
+            (__fmul_rn(v[i].z, v[i].z) + __fmul_rn(v[i].w, v[i].w));
+    }
+    ss = row_reduce_sum(ss, red0);
+    const float rms = 1.0f / sqrtf(ss / (float)C + eps);
+    if (active) {
+      f32x4* y4 = reinterpret_cast<f32x4*>(Y + row * (int64_t)C);
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int j = i * TPR + t;
+        if (j < C4) {
+          f32x4 o;
+          o.x = __fmul_rn(__fmul_rn(v[i].x, rms), g[i].x);
+          o.y = __fmul_rn(__fmul_rn(v[i].y, rms), g[i].y);
+          o.z = __fmul_rn(__fmul_rn(v[i].z, rms), g[i].z);
+          o.w = __fmul_rn(__fmul_rn(v[i].w, rms), g[i].w);
+          y4[j] = o;
+        }
+      }
+    }
+  } else {  // softmax
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) m = fmaxf(m, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
+    m = row_reduce_max(m, red0);
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      v[i].x = expf(v[i].x - m);
+      v[i].y = expf(v[i].y - m);
+      v[i].z = expf(v[i].z - m);
+      v[i].w = expf(v[i].w - m);
+      s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    }
+    s = row_reduce_sum(s, red1);
+    if (active) {
+      f32x4* y4 = reinterpret_cast<f32x4*>(Y + row * (int64_t)C);
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int j = i * TPR + t;
+        if (j < C4) y4[j] = f32x4{v[i].x / s, v[i].y / s, v[i].z / s, v[i].w / s};
+      }
+    }
+  }
+}
+
+// Any row length: the row is streamed (twice for RMSNorm, three times for softmax) with
+// scalar coalesced loads. Used only when C is not a multiple of 4 or does not fit registers.
+template <int OP>
+__global__ void __launch_bounds__(256)
+    rows_stream_kernel(const float* __restrict__ X, const float* __restrict__ Wg, float* __restrict__ Y, int L,
+                       int C, float eps) {
+  __shared__ float red0[4];
+  __shared__ float red1[4];
+  const int tid = threadIdx.x, wave = tid >> 6;
+  const int64_t row = blockIdx.x;
+  if (row >= L) return;  // uniform per workgroup: one row per workgroup
+  const float* x = X + row * (int64_t)C;
+  auto block_sum = [&](float s, float* slots) {
+    s = wave_sum(s);
+    if ((tid & 63) == 0) slots[wave] = s;
+    __syncthreads();
+    return ((slots[0] + slots[1]) + slots[2]) + slots[3];
+  };
+  auto block_max = [&](float m, float* slots) {
+    m = wave_max(m);
+    if ((tid & 63) == 0) slots[wave] = m;
+    __syncthreads();
+    return fmaxf(fmaxf(slots[0], slots[1]), fmaxf(slots[2], slots[3]));
+  };
+  if constexpr (OP == 0) {
+    float s = 0.f;
+    for (int c = tid; c < C; c += 256) s += x[c];
+    s = block_sum(s, red0);
+    if (tid == 0) Y[row] = s;
+  } else if constexpr (OP == 1) {
+    float ss = 0.f;
+    for (int c = tid; c < C; c += 256) ss += __fmul_rn(x[c], x[c]);
+    ss = block_sum(ss, red0);
+    const float rms = 1.0f / sqrtf(ss / (float)C + eps);
+    float* y = Y + row * (int64_t)C;
+    for (int c = tid; c < C; c += 256) y[c] = __fmul_rn(__fmul_rn(x[c], rms), Wg[c]);
+  } else {
+    float m = -INFINITY;
+    for (int c = tid; c < C; c += 256) m = fmaxf(m, x[c]);
+    m = block_max(m, red0);
+    float s = 0.f;
+    for (int c = tid; c < C; c += 256) s += expf(x[c] - m);
+    s = block_sum(s, red1);
+    float* y = Y + row * (int64_t)C;
+    for (int c = tid; c < C; c += 256) y[c] = expf(x[c] - m) / s;
+  }
+}
+
+// Standalone channelscale (reference src/codegen_hip.cpp:2329-2335): Y[i*C+c] = X[i*C+c]*S[c].
+__global__ void __launch_bounds__(256)
+    channelscale4_kernel(const f32x4* __restrict__ X, const float* __restrict__ S, f32x4* __restrict__ Y,
+                         int64_t n4, int C) {
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride) {
+    const int c = (int)((i * 4) % C);
+    const f32x4 x = X[i];
+    Y[i] = f32x4{x.x * S[c], x.y * S[c + 1], x.z * S[c + 2], x.w * S[c + 3]};
+  }
+}
+__global__ void __launch_bounds__(256)
+    channelscale1_kernel(const float* __restrict__ X, const float* __restrict__ S, float* __restrict__ Y, int64_t n,
+                         int C) {
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) Y[i] = X[i] * S[i % C];
+}
+
+// 1-D reduce, pass 1: partial p sums the contiguous chunk [p*chunk, min((p+1)*chunk, n)).
+__global__ void __launch_bounds__(kReduceThreads)
+    reduce_part_kernel(const float* __restrict__ X, float* __restrict__ P, int64_t n, int64_t chunk) {
+  __shared__ float slots[kReduceThreads / 64];
+  const int tid = threadIdx.x;
+  const int64_t b = (int64_t)blockIdx.x * chunk;
+  const int64_t e = b + chunk < n ? b + chunk : n;
+  float s = 0.f;
+  if ((chunk & 3) == 0 && (((uintptr_t)X) & 15) == 0) {
+    const f32x4* x4 = reinterpret_cast<const f32x4*>(X + b);
+    const int64_t full4 = (e - b) >> 2;
+    for (int64_t i = tid; i < full4; i += kReduceThreads) {
+      const f32x4 v = x4[i];
+      s += (v.x + v.y) + (v.z + v.w);
+    }
+    for (int64_t i = b + (full4 << 2) + tid; i < e; i += kReduceThreads) s += X[i];
+  } else {
+    for (int64_t i = b + tid; i < e; i += kReduceThreads) s += X[i];
+  }
+  s = wave_sum(s);
+  if ((tid & 63) == 0) slots[tid >> 6] = s;
+  __syncthreads();
+  if (tid == 0) {
+    float r = slots[0];
+    for (int w = 1; w < kReduceThreads / 64; ++w) r += slots[w];
+    P[blockIdx.x] = r;
+  }
+}
+// Pass 2: one workgroup folds the partials (thread t takes t, t+256, ...), then in wave order.
+__global__ void __launch_bounds__(kReduceThreads)
+    reduce_fold_kernel(const float* __restrict__ P, float* __restrict__ Y, int np) {
+  __shared__ float slots[kReduceThreads / 64];
+  const int tid = threadIdx.x;
+  float s = 0.f;
+  for (int i = tid; i < np; i += kReduceThreads) s += P[i];
+  s = wave_sum(s);
+  if ((tid & 63) == 0) slots[tid >> 6] = s;
+  __syncthreads();
+  if (tid == 0) {
+    float r = slots[0];
+    for (int w = 1; w < kReduceThreads / 64; ++w) r += slots[w];
+    Y[0] = r;
+  }
+}
+
+}  // namespace uk::kern
+
+namespace uk {
+
+namespace {
+template <int TPR, int NV>
+hipError_t rows_dispatch_op(RowOp op, const float* X, const float* W, float* Y, int64_t L, int64_t C, float eps,
+                            hipStream_t s) {
+  constexpr int WG = TPR < 256 ? 256 : TPR;
+  constexpr int RPW = WG / TPR;
+  const int64_t grid = (L + RPW - 1) / RPW;
+  switch (op) {
+    case RowOp::Sum:
+      hipLaunchKernelGGL((kern::rows_kernel<TPR, NV, 0>), dim3((unsigned)grid), dim3(WG), 0, s, X, W, Y, (int)L,
+                         (int)C, eps);
+      break;
+    case RowOp::RmsNorm:
+      hipLaunchKernelGGL((kern::rows_kernel<TPR, NV, 1>), dim3((unsigned)grid), dim3(WG), 0, s, X, W, Y, (int)L,
+                         (int)C, eps);
+      break;
+    case RowOp::Softmax:
+      hipLaunchKernelGGL((kern::rows_kernel<TPR, NV, 2>), dim3((unsigned)grid), dim3(WG), 0, s, X, W, Y, (int)L,
+                         (int)C, eps);
+      break;
+  }
+  return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_rows(const Plan& p, RowOp op, const float* X, const float* W, float* Y, int64_t L, int64_t C,
+                       float eps, hipStream_t s) {
+  if (L <= 0 || C <= 0 || L > INT32_MAX || C > INT32_MAX) return hipErrorInvalidValue;
+  if (op == RowOp::RmsNorm && !W) return hipErrorInvalidValue;
+  if (p.family == Family::RowsStream) {
+    if (L > 0x7fffffff) return hipErrorInvalidValue;
+    switch (op) {
+      case RowOp::Sum:
+        hipLaunchKernelGGL(kern::rows_stream_kernel<0>, dim3((unsigned)L), dim3(256), 0, s, X, W, Y, (int)L, (int)C,
+                           eps);
+        break;
+      case RowOp::RmsNorm:
+        hipLaunchKernelGGL(kern::rows_stream_kernel<1>, dim3((unsigned)L), dim3(256), 0, s, X, W, Y, (int)L, (int)C,
+                           eps);
+        break;
+      case RowOp::Softmax:
+        hipLaunchKernelGGL(kern::rows_stream_kernel<2>, dim3((unsigned)L), dim3(256), 0, s, X, W, Y, (int)L, (int)C,
+                           eps);
+        break;
+    }
+    return hipGetLastError();
+  }
+  if (p.family != Family::Rows || p.variant < 0 || p.variant >= kNumRowsVariants) return hipErrorInvalidValue;
+  const RowsVariant v = kRowsVariants[p.variant];
+  // The register-resident kernel reads float4 at row*C + 4j: rows must be 16-byte aligned and
+  // the row must fit the variant's capacity.
+  if ((C & 3) != 0 || C > (int64_t)v.tpr * v.nv * 4) return hipErrorInvalidValue;
+  if ((((uintptr_t)X) & 15) || (((uintptr_t)Y) & 15) || (W && (((uintptr_t)W) & 15))) return hipErrorInvalidValue;
+  switch (p.variant) {
+#define UK_ROWS_CASE(I)                                                                                 \
+  case I:                                                                                               \
+    return rows_dispatch_op<kRowsVariants[I].tpr, kRowsVariants[I].nv>(op, X, W, Y, L, C, eps, s);
+    UK_ROWS_CASE(0)
+    UK_ROWS_CASE(1)
+    UK_ROWS_CASE(2)
+    UK_ROWS_CASE(3)
+    UK_ROWS_CASE(4)
+    UK_ROWS_CASE(5)
+    UK_ROWS_CASE(6)
+    UK_ROWS_CASE(7)
+    UK_ROWS_CASE(8)
+    UK_ROWS_CASE(9)
+    UK_ROWS_CASE(10)
+    UK_ROWS_CASE(11)
+    UK_ROWS_CASE(12)
+    UK_ROWS_CASE(13)
+    UK_ROWS_CASE(14)
+    UK_ROWS_CASE(15)
+#undef UK_ROWS_CASE
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_channelscale(const float* X, const float* S, float* Y, int64_t L, int64_t C, hipStream_t s) {
+  if (L <= 0 || C <= 0 || C > INT32_MAX) return hipErrorInvalidValue;
+  const int64_t n = L * C;
+  const bool v4 = (C & 3) == 0 && !(((uintptr_t)X) & 15) && !(((uintptr_t)Y) & 15);
+  const int64_t units = v4 ? n / 4 : n;
+  int64_t grid = (units + 255) / 256;
+  if (grid > 256 * 32) grid = 256 * 32;  // grid-stride beyond 32 workgroups per CU
+  if (v4)
+    hipLaunchKernelGGL(kern::channelscale4_kernel, dim3((unsigned)grid), dim3(256), 0, s,
+                       reinterpret_cast<const kern::f32x4*>(X), S, reinterpret_cast<kern::f32x4*>(Y), units, (int)C);
+  else
+    hipLaunchKernelGGL(kern::channelscale1_kernel, dim3((unsigned)grid), dim3(256), 0, s, X, S, Y, n, (int)C);
+  return hipGetLastError();
+}
+
+hipError_t launch_reduce1d(const float* X, float* partials, float* Y, int64_t n, hipStream_t s) {
+  if (n < 0 || !partials) return hipErrorInvalidValue;
+  int64_t chunk = (n + kReduceParts - 1) / kReduceParts;
+  chunk = (chunk + 3) & ~int64_t(3);
+  if (chunk < 4) chunk = 4;
+  const int64_t np = n == 0 ? 1 : (n + chunk - 1) / chunk;  // <= kReduceParts
+  hipLaunchKernelGGL(kern::reduce_part_kernel, dim3((unsigned)np), dim3(kReduceThreads), 0, s, X, partials, n, chunk);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern::reduce_fold_kernel, dim3(1), dim3(kReduceThreads), 0, s, partials, Y, (int)np);
+  return hipGetLastError();
+}
+
+}  // namespace uk

@@ -1,0 +1,29 @@
+// Host-side launchers of the kernel families (internal to libunikern_hip.so).
+// Every launcher validates what its kernel's grid and indexing assume before it enqueues,
+// and returns hipErrorInvalidValue instead of launching a shape the kernel does not cover.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "host/uk_core.hpp"
+
+namespace uk {
+
+enum class RowOp : int { Sum = 0, RmsNorm = 1, Softmax = 2 };
+
+hipError_t launch_rows(const Plan& p, RowOp op, const float* X, const float* W, float* Y, int64_t L, int64_t C,
+                       float eps, hipStream_t s);
+hipError_t launch_channelscale(const float* X, const float* S, float* Y, int64_t L, int64_t C, hipStream_t s);
+hipError_t launch_reduce1d(const float* X, float* partials, float* Y, int64_t n, hipStream_t s);
+
+hipError_t launch_gemm_f16(const Plan& p, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
+                           hipStream_t s);
+hipError_t launch_gemm_generic(DType dt, Layout lay, const void* A, const void* B, void* C, int64_t M, int64_t N,
+                               int64_t K, hipStream_t s);
+hipError_t launch_q8_gemm(const Plan& p, const void* X, const void* Wq, float* Y, int64_t M, int64_t N, int64_t K,
+                          hipStream_t s);
+hipError_t launch_conv_igemm(const Plan& p, const Shape& sh, Layout lay, const float* X, const float* Wt,
+                             const float* scale, float* Y, hipStream_t s);
+
+}  // namespace uk

@@ -1,0 +1,61 @@
+// Compiled kernel variant tables. The solver enumerates exactly these (its candidate set is
+// what was compiled, so a plan can never name a kernel that does not exist) and the kernel
+// files instantiate exactly these.
+#pragma once
+
+namespace uk {
+
+// Row family (row-sum, RMSNorm, softmax with the row held in registers).
+// tpr: threads per row (whole wavefronts), nv: float4 registers per thread.
+// A workgroup is max(tpr, 256) threads, i.e. 256/tpr rows per workgroup when tpr < 256.
+struct RowsVariant {
+  int tpr, nv;
+};
+constexpr RowsVariant kRowsVariants[] = {
+    {64, 1},   {64, 2},   {64, 4},   {64, 8},  {64, 16}, {128, 4}, {128, 8}, {256, 1},
+    {256, 2},  {256, 4},  {256, 8},  {512, 2}, {512, 4}, {1024, 1}, {1024, 2}, {1024, 4},
+};
+constexpr int kNumRowsVariants = sizeof(kRowsVariants) / sizeof(kRowsVariants[0]);
+constexpr int kRowsStreamThreads = 256;
+
+// 1-D reduce: pass-1 partial count and threads.
+constexpr int kReduceParts = 2048;
+constexpr int kReduceThreads = 256;
+
+// f16 MFMA GEMM, layout TN (A[M][K], B stored [N][K]), v_mfma_f32_32x32x16_f16.
+// bm x bn x bk macro tile; wm x wn waves; stages of LDS buffering.
+struct GemmF16Variant {
+  int bm, bn, bk, wm, wn, stages;
+};
+constexpr GemmF16Variant kGemmF16Variants[] = {
+    {256, 256, 64, 2, 2, 2},
+    {256, 128, 64, 2, 2, 2},
+    {128, 128, 64, 2, 2, 2},
+};
+constexpr int kNumGemmF16Variants = sizeof(kGemmF16Variants) / sizeof(kGemmF16Variants[0]);
+
+// Generic MFMA GEMM (any M, N, K; NT or TN; fp16 or fp32 inputs): 64x64 tiles, 4 waves.
+constexpr int kGemmGenericTile = 64;
+
+// Q8_0 skinny GEMM: 16 output columns (weight rows) per wavefront step, split-K.
+struct Q8Variant {
+  int waves, kblocks;  // waves per workgroup, 32-element blocks per wavefront
+};
+constexpr Q8Variant kQ8Variants[] = {
+    {4, 8}, {4, 16}, {4, 32}, {8, 8}, {8, 16},
+};
+constexpr int kNumQ8Variants = sizeof(kQ8Variants) / sizeof(kQ8Variants[0]);
+
+// Implicit-GEMM conv on f32 MFMA (v_mfma_f32_16x16x4_f32): bm output pixels x bn output
+// channels per workgroup, bk reduction slice.
+struct ConvVariant {
+  int bm, bn, bk, waves;
+};
+constexpr ConvVariant kConvVariants[] = {
+    {64, 64, 16, 4},
+    {128, 64, 16, 4},
+    {32, 64, 16, 2},
+};
+constexpr int kNumConvVariants = sizeof(kConvVariants) / sizeof(kConvVariants[0]);
+
+}  // namespace uk
