@@ -11,7 +11,9 @@
 //     8 rows x 128 B into 1 KiB of LDS; the 16-byte chunk index is XOR-swizzled by row on the
 //     global side, so the MFMA fragment reads (ds_read_b128, 32 rows at one k offset) hit
 //     distinct banks.
-//   * STAGES-deep LDS ring (2 x 64 KiB for 256x256x64), one barrier per k-tile.
+//   * STAGES-deep LDS ring (4 x 32 KiB for 256x256x32): the DMA runs STAGES-1 k-tiles ahead,
+//     with partial vmcnt waits, and one barrier per k-tile; MFMA fragments are double
+//     buffered in registers so LDS reads for the next k-step overlap the current MFMAs.
 //   * workgroup -> tile mapping is XCD-aware: workgroup i runs on XCD i % 8, so ids are
 //     regrouped so each XCD owns a compact block of tiles and shares A/B panels in its L2.
 //   * the MFMA computes C^T tiles (B fragment as the first operand), so each lane holds four
@@ -37,42 +39,65 @@ struct GemmF16Cfg {
   static constexpr int kWTN = BN / WN;  // wave tile cols (N)
   static constexpr int kFM = kWTM / 32;
   static constexpr int kFN = kWTN / 32;
+  static constexpr int kKK = BK / 16;   // MFMA k-steps per k-tile
   static constexpr int kRowBytes = BK * 2;
   static constexpr int kChunks = kRowBytes / 16;  // 16-byte chunks per LDS row
   static constexpr int kRowsPerInst = 1024 / kRowBytes;
   static constexpr int kStageBytes = (BM + BN) * kRowBytes;
+  static constexpr int kInstsA = BM / kRowsPerInst / kWaves;  // DMA instructions per wave per k-tile
+  static constexpr int kInstsB = BN / kRowsPerInst / kWaves;
+  static constexpr int kInsts = kInstsA + kInstsB;
   static constexpr int kPitch = kWTN * 2 + 16;  // epilogue staging row pitch (bytes)
   static constexpr int kEpiBytes = kWaves * kWTM * kPitch;
   static constexpr int kLdsBytes = (STAGES * kStageBytes > kEpiBytes) ? STAGES * kStageBytes : kEpiBytes;
   static_assert(kWTM % 32 == 0 && kWTN % 32 == 0, "wave tile must be whole 32x32 MFMA tiles");
-  static_assert(BK % 16 == 0 && kChunks <= 8 && 1024 % kRowBytes == 0, "BK must be 16..64");
-  static_assert(BM % kRowsPerInst == 0 && BN % kRowsPerInst == 0, "tile rows per DMA instruction");
+  static_assert(BK % 32 == 0 && kChunks <= 8 && 1024 % kRowBytes == 0, "BK must be 32 or 64");
+  static_assert(kKK % 2 == 0, "fragment double buffering alternates k-steps");
+  static_assert(BM % (kRowsPerInst * kWaves) == 0 && BN % (kRowsPerInst * kWaves) == 0,
+                "DMA instructions must split evenly over the wavefronts");
+  static_assert(STAGES >= 3, "the ring prefetches at least two k-tiles ahead");
+  static_assert((STAGES - 2) * kInsts <= 63, "outstanding DMA must fit the vmcnt counter");
 };
 
-__device__ __forceinline__ int swz(int row, int chunks) { return (row & (chunks - 1)); }
+// Physical 16-byte chunk of logical chunk c in LDS row r: c ^ f(r). SWZ picks f for the bank
+// geometry (0: r, 1: r >> 1, 2: r >> 2, each masked to the chunk count).
+template <int SWZ, int CHUNKS>
+__device__ __forceinline__ int swz(int r) {
+  if constexpr (SWZ == 0) return r & (CHUNKS - 1);
+  else if constexpr (SWZ == 1) return (r >> 1) & (CHUNKS - 1);
+  else return (r >> 2) & (CHUNKS - 1);
+}
 
-// Issue the DMA for a rows x BK tile starting at g (row pitch ld elements) into LDS dst.
-template <int ROWS, int BK, int WAVES>
+// s_waitcnt vmcnt(N) with expcnt/lgkmcnt left unconstrained (gfx9 encoding: vmcnt in bits
+// 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Issue the DMA for a ROWS x BK tile starting at g (row pitch ld elements) into LDS dst:
+// instruction i of this wave moves 1 KiB = kRowsPerInst rows; lane l fills physical chunk
+// l % kChunks of row l / kChunks, fetching the logical chunk that lands there.
+template <int ROWS, int BK, int WAVES, int SWZ>
 __device__ __forceinline__ void dma_tile(const _Float16* __restrict__ g, int64_t ld, char* dst, int wave, int lane) {
   constexpr int kRowBytes = BK * 2;
   constexpr int kChunks = kRowBytes / 16;
   constexpr int kRowsPerInst = 1024 / kRowBytes;
   constexpr int kInsts = ROWS / kRowsPerInst;
-  static_assert(kInsts % WAVES == 0, "DMA instructions must split evenly over the wavefronts");
-  const int rr = lane / kChunks;      // row within the instruction's row group
-  const int p = lane % kChunks;       // physical chunk this lane fills
+  const int rr = lane / kChunks;
+  const int p = lane % kChunks;
   const int w = __builtin_amdgcn_readfirstlane(wave);
 #pragma unroll
   for (int t = 0; t < kInsts / WAVES; ++t) {
     const int ins = t * WAVES + w;
     const int r = ins * kRowsPerInst + rr;
-    const int c = p ^ swz(r, kChunks);  // logical chunk stored at physical chunk p
-    const _Float16* src = g + (int64_t)r * ld + c * 8;
-    __builtin_amdgcn_global_load_lds(src, (lds_void*)(dst + ins * 1024), 16, 0, 0);
+    const int c = p ^ swz<SWZ, kChunks>(r);
+    __builtin_amdgcn_global_load_lds(g + (int64_t)r * ld + c * 8, (lds_void*)(dst + ins * 1024), 16, 0, 0);
   }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int STAGES>
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int SWZ>
 __global__ void __launch_bounds__(WM* WN * 64, 1)
     gemm_f16_tn_kernel(const _Float16* __restrict__ A, const _Float16* __restrict__ B, _Float16* __restrict__ C,
                        int M, int N, int K, int tiles_m, int tiles_n) {
@@ -108,52 +133,71 @@ __global__ void __launch_bounds__(WM* WN * 64, 1)
 #pragma unroll
     for (int j = 0; j < Cfg::kFN; ++j) acc[i][j] = f32x16{};
 
-  const int KT = K / BK;
-#pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s) {
-    if (s < KT) {
-      char* st = lds + s * Cfg::kStageBytes;
-      dma_tile<BM, BK, Cfg::kWaves>(Ag + s * BK, K, st, wave, lane);
-      dma_tile<BN, BK, Cfg::kWaves>(Bg + s * BK, K, st + BM * Cfg::kRowBytes, wave, lane);
-    }
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
+  auto issue = [&](int t) {
+    char* st = lds + (t % STAGES) * Cfg::kStageBytes;
+    dma_tile<BM, BK, Cfg::kWaves, SWZ>(Ag + (int64_t)t * BK, K, st, wave, lane);
+    dma_tile<BN, BK, Cfg::kWaves, SWZ>(Bg + (int64_t)t * BK, K, st + BM * Cfg::kRowBytes, wave, lane);
+  };
 
-  const int frow = lane & 31;      // fragment row within a 32-row MFMA tile
-  const int fchunk = lane >> 5;    // which 8-element half of the 16-wide k step
-  for (int kt = 0; kt < KT; ++kt) {
-    const int nxt = kt + STAGES - 1;
-    if (nxt < KT) {
-      char* st = lds + (nxt % STAGES) * Cfg::kStageBytes;
-      dma_tile<BM, BK, Cfg::kWaves>(Ag + nxt * BK, K, st, wave, lane);
-      dma_tile<BN, BK, Cfg::kWaves>(Bg + nxt * BK, K, st + BM * Cfg::kRowBytes, wave, lane);
-    }
-    const char* As = lds + (kt % STAGES) * Cfg::kStageBytes;
+  // Fragment registers, double buffered across k-steps (and across k-tiles).
+  const int frow = lane & 31;    // row within a 32-row MFMA tile
+  const int fhalf = lane >> 5;   // which 8-element half of the 16-wide k-step
+  f16x8 fa[2][Cfg::kFM], fb[2][Cfg::kFN];
+  auto load_frags = [&](f16x8 (&a)[Cfg::kFM], f16x8 (&b)[Cfg::kFN], int t, int kk) {
+    const char* As = lds + (t % STAGES) * Cfg::kStageBytes;
     const char* Bs = As + BM * Cfg::kRowBytes;
+    const int c = kk * 2 + fhalf;
 #pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
-      const int c = kk * 2 + fchunk;
-      f16x8 a[Cfg::kFM], b[Cfg::kFN];
+    for (int i = 0; i < Cfg::kFM; ++i) {
+      const int r = wm * Cfg::kWTM + i * 32 + frow;
+      a[i] = *reinterpret_cast<const f16x8*>(As + r * Cfg::kRowBytes + ((c ^ swz<SWZ, Cfg::kChunks>(r)) << 4));
+    }
 #pragma unroll
-      for (int i = 0; i < Cfg::kFM; ++i) {
-        const int r = wm * Cfg::kWTM + i * 32 + frow;
-        a[i] = *reinterpret_cast<const f16x8*>(As + r * Cfg::kRowBytes + ((c ^ swz(r, Cfg::kChunks)) << 4));
-      }
+    for (int j = 0; j < Cfg::kFN; ++j) {
+      const int r = wn * Cfg::kWTN + j * 32 + frow;
+      b[j] = *reinterpret_cast<const f16x8*>(Bs + r * Cfg::kRowBytes + ((c ^ swz<SWZ, Cfg::kChunks>(r)) << 4));
+    }
+  };
+
+  const int KT = K / BK;
+  // Prologue: tiles 0 .. STAGES-2 in flight; wait for tile 0 only.
 #pragma unroll
-      for (int j = 0; j < Cfg::kFN; ++j) {
-        const int r = wn * Cfg::kWTN + j * 32 + frow;
-        b[j] = *reinterpret_cast<const f16x8*>(Bs + r * Cfg::kRowBytes + ((c ^ swz(r, Cfg::kChunks)) << 4));
-      }
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < KT) issue(s);
+  if (KT >= STAGES - 1)
+    wait_vmcnt<(STAGES - 2) * Cfg::kInsts>();
+  else
+    wait_vmcnt<0>();
+  __syncthreads();
+  load_frags(fa[0], fb[0], 0, 0);
+
+  for (int kt = 0; kt < KT; ++kt) {
+    // Tile kt+1 must have landed (this wave's DMA) and be visible (everyone's): its first
+    // fragments are prefetched during this iteration. The barrier also retires every read of
+    // tile kt-1, whose slot the DMA below overwrites.
+    if (kt + 1 < KT) {
+      if (kt + STAGES - 2 < KT)
+        wait_vmcnt<(STAGES - 3) * Cfg::kInsts>();
+      else
+        wait_vmcnt<0>();
+    }
+    __syncthreads();
+    if (kt + STAGES - 1 < KT) issue(kt + STAGES - 1);
+#pragma unroll
+    for (int kk = 0; kk < Cfg::kKK; ++kk) {
+      const int cur = kk & 1;
+      if (kk + 1 < Cfg::kKK)
+        load_frags(fa[cur ^ 1], fb[cur ^ 1], kt, kk + 1);
+      else if (kt + 1 < KT)
+        load_frags(fa[cur ^ 1], fb[cur ^ 1], kt + 1, 0);
 #pragma unroll
       for (int i = 0; i < Cfg::kFM; ++i)
 #pragma unroll
         for (int j = 0; j < Cfg::kFN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[j], a[i], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[cur][j], fa[cur][i], acc[i][j], 0, 0, 0);
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
   }
+  __syncthreads();
 
   // Epilogue. acc[i][j] holds C^T: lane -> row m = i*32 + (lane & 31) of the wave tile and
   // columns n = j*32 + 8*g + 4*(lane >> 5) + {0..3} for register group g = r / 4.
@@ -249,7 +293,7 @@ hipError_t gemm_f16_variant(const void* A, const void* B, void* C, int64_t M, in
   constexpr GemmF16Variant v = kGemmF16Variants[I];
   using Cfg = kern::GemmF16Cfg<v.bm, v.bn, v.bk, v.wm, v.wn, v.stages>;
   const int tiles_m = int(M / v.bm), tiles_n = int(N / v.bn);
-  hipLaunchKernelGGL((kern::gemm_f16_tn_kernel<v.bm, v.bn, v.bk, v.wm, v.wn, v.stages>),
+  hipLaunchKernelGGL((kern::gemm_f16_tn_kernel<v.bm, v.bn, v.bk, v.wm, v.wn, v.stages, v.swz>),
                      dim3((unsigned)(tiles_m * tiles_n)), dim3(Cfg::kThreads), 0, s,
                      static_cast<const _Float16*>(A), static_cast<const _Float16*>(B), static_cast<_Float16*>(C),
                      (int)M, (int)N, (int)K, tiles_m, tiles_n);
@@ -268,9 +312,18 @@ hipError_t launch_gemm_f16(const Plan& p, const void* A, const void* B, void* C,
   if ((((uintptr_t)A) | ((uintptr_t)B) | ((uintptr_t)C)) & 15) return hipErrorInvalidValue;
   if ((M / v.bm) * (N / v.bn) > INT32_MAX) return hipErrorInvalidValue;
   switch (p.variant) {
-    case 0: return gemm_f16_variant<0>(A, B, C, M, N, K, s);
-    case 1: return gemm_f16_variant<1>(A, B, C, M, N, K, s);
-    case 2: return gemm_f16_variant<2>(A, B, C, M, N, K, s);
+#define UK_GEMM_CASE(I) \
+  case I:                 \
+    return gemm_f16_variant<I>(A, B, C, M, N, K, s);
+    UK_GEMM_CASE(0)
+    UK_GEMM_CASE(1)
+    UK_GEMM_CASE(2)
+    UK_GEMM_CASE(3)
+    UK_GEMM_CASE(4)
+    UK_GEMM_CASE(5)
+    UK_GEMM_CASE(6)
+    UK_GEMM_CASE(7)
+#undef UK_GEMM_CASE
     default: return hipErrorInvalidValue;
   }
 }

@@ -23,14 +23,20 @@ constexpr int kReduceParts = 2048;
 constexpr int kReduceThreads = 256;
 
 // f16 MFMA GEMM, layout TN (A[M][K], B stored [N][K]), v_mfma_f32_32x32x16_f16.
-// bm x bn x bk macro tile; wm x wn waves; stages of LDS buffering.
+// bm x bn x bk macro tile; wm x wn waves; stages of LDS buffering; swz selects the LDS
+// XOR swizzle (0: row, 1: row >> 1, 2: row >> 2) for the bank geometry.
 struct GemmF16Variant {
-  int bm, bn, bk, wm, wn, stages;
+  int bm, bn, bk, wm, wn, stages, swz;
 };
 constexpr GemmF16Variant kGemmF16Variants[] = {
-    {256, 256, 64, 2, 2, 2},
-    {256, 128, 64, 2, 2, 2},
-    {128, 128, 64, 2, 2, 2},
+    {256, 256, 32, 2, 2, 4, 1},
+    {256, 256, 32, 2, 2, 4, 2},
+    {256, 256, 32, 2, 2, 4, 0},
+    {256, 256, 32, 2, 4, 4, 1},
+    {256, 128, 32, 2, 2, 4, 1},
+    {256, 128, 64, 2, 2, 3, 1},
+    {128, 128, 64, 2, 2, 3, 1},
+    {128, 128, 32, 2, 2, 4, 1},
 };
 constexpr int kNumGemmF16Variants = sizeof(kGemmF16Variants) / sizeof(kGemmF16Variants[0]);
 
