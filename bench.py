@@ -11,7 +11,8 @@ Timed region: barrier (device synchronize), K steps enqueued kernel by kernel (K
 K RMSNorms, K softmaxes, each segment between HIP events on the launch stream), synchronize.
 value = algorithmic bytes of K steps / event time of the K steps. Per-kernel averages feed the
 roofline of the dominant kernel. The f16 GEMM 4096^3 is timed the same way and
-reported under "secondary" (TFLOP/s and fraction of the dense f16 MFMA peak).
+reported under "secondary" (TFLOP/s and fraction of the dense f16 MFMA peak), with the conv2d
+(configs[3], f32 MFMA) and the Q8_0 decode GEMMs (configs[4], GB/s of weight bytes).
 
 cpu_baseline: the reference's own CPU loops (oracle/_ref, compiled from the reference sources;
 the C restatement in oracle/ when that build is absent) on the host, one thread, over a bounded
@@ -37,6 +38,7 @@ METRIC = "f16 GEMM TFLOP/s + %MFMA peak; rmsnorm/softmax GB/s + %HBM peak (1 GPU
 SEED = 20261201
 HBM_PEAK_GBS = 8000.0
 F16_PEAK_TFLOPS = 2516.5824
+F32_PEAK_TFLOPS = 157.2864
 L = Cc = 4096
 
 
@@ -134,41 +136,99 @@ def bench_rows(uk, O, steps: int, warmup: int, stream):
     return stats, total_ms, wall / steps, step_bytes, verified, sets
 
 
-def bench_gemm(uk, O, steps: int, warmup: int, stream):
-    M = N = K = 4096
-    A = O.f16_bits(O.uniform(M * K, SEED + 20, -1.0, 1.0)).reshape(M, K)
-    B = O.f16_bits(O.uniform(N * K, SEED + 21, -1.0, 1.0)).reshape(N, K)
-    d = uk.make_desc("gemm", [M, N, K], dtype="fp16", layout="TN")
+def _time_op(uk, d, host_inputs, out_bytes, steps, warmup, stream, min_set_bytes=512 << 20):
+    """Upload the inputs into enough device sets to exceed min_set_bytes, launch once (set 0) for
+    verification, then time `steps` launches over the rotating sets with HIP events."""
+    set_bytes = sum(a.nbytes for a in host_inputs) + out_bytes
+    sets = int(min(64, max(2, min_set_bytes // set_bytes + 2)))
+    ins = [[uk.DeviceBuffer.from_array(a) for a in host_inputs] for _ in range(sets)]
+    outs = [uk.DeviceBuffer(out_bytes) for _ in range(sets)]
     sol = uk.solve(d)
-    sets = (512 << 20) // (3 * M * K * 2) + 2
-    As = [uk.DeviceBuffer.from_array(A) for _ in range(sets)]
-    Bs = [uk.DeviceBuffer.from_array(B) for _ in range(sets)]
-    Cs = [uk.DeviceBuffer(M * N * 2) for _ in range(sets)]
-    flat = [p for a, b in zip(As, Bs) for p in (a.ptr.value, b.ptr.value)]
-    outs = [c.ptr.value for c in Cs]
-    _launch_n(uk, d, sol.plan, flat[:2], 2, outs[:1], 1, stream)
+    n_in = len(host_inputs)
+    flat = [b.ptr.value for s_ in ins for b in s_]
+    optr = [o.ptr.value for o in outs]
+    _launch_n(uk, d, sol.plan, flat[:n_in], n_in, optr[:1], 1, stream)
     uk._check(uk.lib.uk_stream_synchronize(stream))
-    rows = np.array([0, 1, 777, 2048, 4095])
-    Cg = O.f16_to_f32(Cs[0].download(np.uint16, (M, N))[rows]).astype(np.float64)
-    R = O.gemm_f16q(A[rows], B, True).astype(np.float64)
-    fro = float(np.linalg.norm(Cg - R) / np.linalg.norm(R))
     e0, e1 = _events(uk)
     if warmup:
-        _launch_n(uk, d, sol.plan, flat, 2, outs, warmup, stream)
+        _launch_n(uk, d, sol.plan, flat, n_in, optr, warmup, stream)
     uk._check(uk.lib.uk_event_record(e0, stream))
-    _launch_n(uk, d, sol.plan, flat, 2, outs, steps, stream)
+    _launch_n(uk, d, sol.plan, flat, n_in, optr, steps, stream)
     uk._check(uk.lib.uk_event_record(e1, stream))
     uk._check(uk.lib.uk_stream_synchronize(stream))
     ms = _elapsed(uk, e0, e1) / steps
     for e in (e0, e1):
         uk.lib.uk_event_destroy(e)
-    for b in As + Bs + Cs:
-        b.free()
+    first_out = outs[0]
+    for s_ in ins:
+        for b in s_:
+            b.free()
+    for o in outs[1:]:
+        o.free()
+    return ms, sol.key, first_out, sets
+
+
+def bench_gemm(uk, O, steps: int, warmup: int, stream):
+    M = N = K = 4096
+    A = O.f16_bits(O.uniform(M * K, SEED + 20, -1.0, 1.0)).reshape(M, K)
+    B = O.f16_bits(O.uniform(N * K, SEED + 21, -1.0, 1.0)).reshape(N, K)
+    d = uk.make_desc("gemm", [M, N, K], dtype="fp16", layout="TN")
+    ms, key, cb, sets = _time_op(uk, d, [A, B], M * N * 2, steps, warmup, stream)
+    rows = np.array([0, 1, 777, 2048, 4095])
+    Cg = O.f16_to_f32(cb.download(np.uint16, (M, N))[rows]).astype(np.float64)
+    cb.free()
+    R = O.gemm_f16q(A[rows], B, True).astype(np.float64)
+    fro = float(np.linalg.norm(Cg - R) / np.linalg.norm(R))
     tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
-    return {"workload": "gemm f16 4096^3, A row-major, B column-major, f32 accumulate, f16 out",
+    return {"workload": "gemm f16 4096^3, A row-major, B column-major, f32 accumulate, f16 out (configs[2])",
             "ms": round(ms, 6), "value": round(tflops, 1), "unit": "TFLOP/s",
-            "frac_mfma_peak": round(tflops / F16_PEAK_TFLOPS, 4), "plan": sol.key, "frobenius_rel": fro,
-            "verified": fro <= 1e-2, "sets": sets}
+            "frac_peak": round(tflops / F16_PEAK_TFLOPS, 4), "peak": F16_PEAK_TFLOPS, "plan": key,
+            "frobenius_rel": fro, "verified": fro <= 1e-2, "sets": sets}
+
+
+def bench_conv(uk, O, steps: int, warmup: int, stream):
+    N, C, H, W, Oc = 8, 64, 56, 56, 64
+    x = O.normal(N * C * H * W, SEED + 30, 0.0, 1.0).reshape(N, C, H, W)
+    w = O.normal(Oc * C * 9, SEED + 31, 0.0, float(np.sqrt(2.0 / (C * 9)))).reshape(Oc, C, 3, 3)
+    s = O.uniform(Oc, SEED + 32, 0.5, 1.5)
+    d = uk.make_desc("conv", [H, W, C, 3, 3, Oc], layout="NCHW", batch=N, pad=1, epilogue="channelscale")
+    ms, key, yb, sets = _time_op(uk, d, [x, w, s], N * Oc * H * W * 4, steps, warmup, stream)
+    y = yb.download(np.float32, (N, Oc, H, W))[:1]
+    yb.free()
+    r = O.conv_nchw(x[:1], w, s, pad=1).astype(np.float64)
+    fro = float(np.linalg.norm(y - r) / np.linalg.norm(r))
+    flops = 2.0 * N * Oc * H * W * C * 9
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"workload": "conv2d NCHW 8x64x56x56 -> 64, 3x3, pad 1, fused channelscale, f32 MFMA (configs[3])",
+            "ms": round(ms, 6), "value": round(tflops, 2), "unit": "TFLOP/s",
+            "frac_peak": round(tflops / F32_PEAK_TFLOPS, 4), "peak": F32_PEAK_TFLOPS, "plan": key,
+            "frobenius_rel": fro, "verified": fro <= 1e-5, "sets": sets}
+
+
+def bench_q8(uk, O, steps: int, warmup: int, stream):
+    import _oracle
+
+    out = []
+    K = 4096
+    for N in (4096, 11008):
+        u = O.uniform(N * K, SEED + 41, 0.0, 1.0)
+        q = ((u * 255.0).astype(np.int32) - 127).astype(np.int8).reshape(N, K)
+        dh = O.f16_bits(O.uniform(N * (K // 32), SEED + 42, 1e-3, 1e-2)).reshape(N, K // 32)
+        blocks = _oracle.q8_0_pack(q, dh)
+        for M in (1, 8, 16):
+            Xh = O.f16_bits(O.normal(M * K, SEED + 40, 0.0, 1.0)).reshape(M, K)
+            d = uk.make_desc("gemm", [M, N, K], dtype="q8_0", layout="TN")
+            ms, key, yb, sets = _time_op(uk, d, [Xh, blocks], M * N * 4, steps, warmup, stream)
+            y = yb.download(np.float32, (M, N)).astype(np.float64)
+            yb.free()
+            r = O.q8_0_gemm(Xh, blocks, N)
+            fro = float(np.linalg.norm(y - r) / np.linalg.norm(r))
+            gbs = blocks.nbytes / (ms * 1e-3) / 1e9
+            out.append({"workload": f"q8_0 skinny GEMM M={M} N={N} K={K} (configs[4])", "ms": round(ms, 6),
+                        "value": round(gbs, 1), "unit": "GB/s of weight bytes", "frac_peak": round(gbs / HBM_PEAK_GBS, 4),
+                        "peak": HBM_PEAK_GBS, "plan": key, "frobenius_rel": fro, "verified": fro <= 1e-5,
+                        "sets": sets})
+    return out
 
 
 def cpu_baseline(O, budget_s: float):
@@ -221,7 +281,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-gemm", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true", help="skip the GEMM, conv and Q8_0 configs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -239,8 +299,11 @@ def main():
     value = step_bytes / (total_ms * 1e-3) / 1e9
     dom = max(stats, key=lambda k: stats[k]["ms"])
     secondary = []
-    if not args.no_gemm:
-        secondary.append(bench_gemm(uk, O, max(10, args.steps // 2), max(5, args.warmup // 2), stream))
+    if not args.no_secondary:
+        sec_steps, sec_warm = max(10, args.steps // 2), max(5, args.warmup // 2)
+        secondary.append(bench_gemm(uk, O, sec_steps, sec_warm, stream))
+        secondary.append(bench_conv(uk, O, sec_steps, sec_warm, stream))
+        secondary.extend(bench_q8(uk, O, args.steps, args.warmup, stream))
     uk.lib.uk_stream_destroy(stream)
 
     traffic = None

@@ -1,0 +1,117 @@
+"""Parity of the implicit-GEMM conv (f32 MFMA, fused channelscale) against the CPU oracle.
+
+Gates: ||y - r||_F / ||r||_F <= 1e-5 against the reference-order loop (src/reference.cpp:6-22
+restated, extended to batch/padding/stride and the channelscale epilogue); on the reference's
+sawtooth inputs every partial sum is exact, so the output must match bit for bit.
+"""
+import numpy as np
+import pytest
+
+import _oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def conv_nchw_gpu(uk, x, w, scale, pad, stride=1, plan=None):
+    N, C, H, W = x.shape
+    Oc, _, Kh, Kw = w.shape
+    d = uk.make_desc("conv", [H, W, C, Kh, Kw, Oc], layout="NCHW", batch=N, pad=pad, stride=stride,
+                     epilogue="channelscale" if scale is not None else "none")
+    Ho, Wo = (H + 2 * pad - Kh) // stride + 1, (W + 2 * pad - Kw) // stride + 1
+    ins = [uk.DeviceBuffer.from_array(x), uk.DeviceBuffer.from_array(w)]
+    if scale is not None:
+        ins.append(uk.DeviceBuffer.from_array(scale))
+    yb = uk.DeviceBuffer(N * Oc * Ho * Wo * 4)
+    yb.fill(0xFF)
+    uk.launch(d, ins, yb, plan=plan)
+    return yb.download(np.float32, (N, Oc, Ho, Wo))
+
+
+def conv_hwc_gpu(uk, x, wt, H, W, C, Kh, Kw, Oc, plan=None):
+    d = uk.make_desc("conv", [H, W, C, Kh, Kw, Oc])
+    yb = uk.DeviceBuffer(Oc * (H - Kh + 1) * (W - Kw + 1) * 4)
+    yb.fill(0xFF)
+    uk.launch(d, [uk.DeviceBuffer.from_array(x), uk.DeviceBuffer.from_array(wt)], yb, plan=plan)
+    return yb.download(np.float32, (Oc, H - Kh + 1, W - Kw + 1))
+
+
+def frob(got, ref):
+    return float(np.linalg.norm(got.astype(np.float64) - ref.astype(np.float64)) /
+                 np.linalg.norm(ref.astype(np.float64)))
+
+
+def rand_conv(N, C, H, W, Oc, Kh, Kw, seed):
+    x = O.normal(N * C * H * W, seed, 0.0, 1.0).reshape(N, C, H, W)
+    w = O.normal(Oc * C * Kh * Kw, seed + 1, 0.0, float(np.sqrt(2.0 / (C * Kh * Kw)))).reshape(Oc, C, Kh, Kw)
+    s = O.uniform(Oc, seed + 2, 0.5, 1.5)
+    return x, w, s
+
+
+def test_baseline_config_nchw_channelscale(gpu):
+    # N=8, C=64, 56x56, Oc=64, 3x3, pad 1, stride 1, channelscale epilogue.
+    x, w, s = rand_conv(8, 64, 56, 56, 64, 3, 3, 20261201 + 30)
+    y = conv_nchw_gpu(gpu, x, w, s, pad=1)
+    r = O.conv_nchw(x, w, s, pad=1)
+    assert frob(y, r) <= 1e-5
+    assert np.all(np.isfinite(y))
+
+
+def test_baseline_shape_exact_mode_bit_exact(gpu):
+    x = O.sawtooth(8 * 64 * 56 * 56, 17, 8).reshape(8, 64, 56, 56)
+    w = O.sawtooth(64 * 64 * 9, 13, 6).reshape(64, 64, 3, 3)
+    s = O.sawtooth(64, 7, 3, bias=1.0)
+    y = conv_nchw_gpu(gpu, x, w, s, pad=1)
+    assert np.array_equal(y.view(np.uint32), O.conv_nchw(x, w, s, pad=1).view(np.uint32))
+
+
+@pytest.mark.parametrize("N,C,H,W,Oc,Kh,Kw,pad,stride", [
+    (1, 3, 9, 7, 10, 3, 3, 1, 1),     # odd channels, Oc < 64, plane not a multiple of 32
+    (2, 70, 12, 12, 70, 3, 3, 1, 1),  # two channel chunks with the small variants, two oc tiles
+    (1, 16, 17, 17, 32, 3, 3, 0, 2),  # stride 2, valid
+    (1, 8, 11, 13, 8, 5, 5, 2, 1),    # 5x5: runtime tap table
+    (3, 32, 8, 8, 64, 1, 1, 0, 1),    # 1x1
+    (1, 1, 3, 3, 1, 3, 3, 0, 1),      # single output
+])
+def test_nchw_shapes(gpu, N, C, H, W, Oc, Kh, Kw, pad, stride):
+    x, w, s = rand_conv(N, C, H, W, Oc, Kh, Kw, 7 + C + Oc)
+    for scale in (s, None):
+        y = conv_nchw_gpu(gpu, x, w, scale, pad=pad, stride=stride)
+        r = O.conv_nchw(x, w, scale, pad=pad, stride=stride)
+        assert frob(y, r) <= 1e-5
+
+
+@pytest.mark.parametrize("vi", range(4))
+def test_every_conv_variant(gpu, vi):
+    p = gpu.Plan()
+    p.family, p.variant = 7, vi
+    x, w, s = rand_conv(2, 40, 20, 20, 64, 3, 3, 100 + vi)
+    y = conv_nchw_gpu(gpu, x, w, s, pad=1, plan=p)
+    assert frob(y, O.conv_nchw(x, w, s, pad=1)) <= 1e-5
+
+
+def test_reference_sample_hwc_exact_mode(gpu):
+    # samples/kml_conv.json: H=W=64, C=32, 3x3, Oc=64, the reference's HWC valid conv.
+    H, W, C, Kh, Kw, Oc = 64, 64, 32, 3, 3, 64
+    x = O.sawtooth(H * W * C, 17, 8)
+    wt = O.sawtooth(Oc * Kh * Kw * C, 13, 6)
+    y = conv_hwc_gpu(gpu, x, wt, H, W, C, Kh, Kw, Oc)
+    r = O.cpu_conv(x, wt, H, W, C, Kh, Kw, Oc)
+    assert np.array_equal(y.view(np.uint32), r.view(np.uint32))
+
+
+@pytest.mark.parametrize("H,W,C,Kh,Kw,Oc", [(64, 64, 32, 3, 3, 64), (10, 7, 5, 3, 2, 9), (5, 5, 1, 5, 5, 1)])
+def test_reference_hwc_random(gpu, H, W, C, Kh, Kw, Oc):
+    x = O.normal(H * W * C, 3 + C, 0.0, 1.0)
+    wt = O.normal(Oc * Kh * Kw * C, 4 + C, 0.0, 0.3)
+    y = conv_hwc_gpu(gpu, x, wt, H, W, C, Kh, Kw, Oc)
+    assert frob(y, O.cpu_conv(x, wt, H, W, C, Kh, Kw, Oc)) <= 1e-5
+
+
+def test_reference_hand_cases(gpu):
+    # tests/acceptance.cpp:1322-1346: 1x1 scale, identity-kernel trace, two-channel dots.
+    y = conv_hwc_gpu(gpu, np.array([1, 2, 3, 4], np.float32), np.array([0.5], np.float32), 2, 2, 1, 1, 1, 1)
+    assert y.ravel().tolist() == [0.5, 1.0, 1.5, 2.0]
+    y = conv_hwc_gpu(gpu, np.arange(1, 10, dtype=np.float32), np.eye(3, dtype=np.float32).ravel(), 3, 3, 1, 3, 3, 1)
+    assert y.ravel().tolist() == [15.0]
+    y = conv_hwc_gpu(gpu, np.array([1, 2, 3, 4], np.float32), np.array([1, 10, -1, 1], np.float32), 1, 2, 2, 1, 1, 2)
+    assert y.ravel().tolist() == [21.0, 43.0, 1.0, 1.0]

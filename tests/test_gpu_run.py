@@ -58,3 +58,29 @@ def test_run_refuses_unsupported(gpu):
     r = gpu.run(gpu.make_desc("softmax", [16, 16], dtype="fp16"))
     assert r.exit_code == 2 and not r.ran
     assert "op_unsupported" in r.log
+
+
+@pytest.mark.parametrize("M", [1, 8, 16])
+@pytest.mark.parametrize("N", [4096, 11008])
+def test_run_q8_0_configs(gpu, M, N):
+    r = gpu.run(gpu.make_desc("gemm", [M, N, 4096], dtype="q8_0", layout="TN"), iters=50)
+    _ok(r)
+    assert r.bound == "hbm" and r.raw.weight_bytes == N * 128 * 34
+    print(r.line)
+
+
+def test_run_conv_config(gpu):
+    d = gpu.make_desc("conv", [56, 56, 64, 3, 3, 64], layout="NCHW", batch=8, pad=1, epilogue="channelscale")
+    r = gpu.run(d, iters=20)
+    _ok(r)
+    assert r.bound == "mfma" and r.err_metric <= 1e-5
+    print(r.line)
+    r = gpu.run(d, exact=True, iters=5)
+    _ok(r)
+    assert r.err_metric == 0
+
+
+def test_run_reference_conv_sample(gpu):
+    r = gpu.run(gpu.make_desc("conv", [64, 64, 32, 3, 3, 64]), exact=True, iters=5)
+    _ok(r)
+    assert r.err_metric == 0

@@ -485,8 +485,9 @@ std::string support_gap(const KmlTree& t) {
         if (t.layout != Layout::TN)
           return "dtype=q8_0 weights are stored one row per output column (layout TN); layout=" +
                  std::string(to_string(t.layout)) + " has no q8_0 kernel";
-        if (t.dims[2] % 32 != 0)
-          return "dtype=q8_0 needs K divisible by the 32-element block; K=" + std::to_string(t.dims[2]);
+        if (t.dims[2] % 64 != 0)
+          return "dtype=q8_0 needs K divisible by 64 (whole pairs of 32-element blocks per row); K=" +
+                 std::to_string(t.dims[2]);
         return "";
       }
       return "dtype=" + dt + " has no gemm kernel (int8 results are refused, as in the reference)";

@@ -24,8 +24,11 @@ namespace uk {
 namespace {
 
 // Effective DRAM latency seen by a streaming wavefront (issue to data), used to turn bytes in
-// flight into sustainable bandwidth.
-constexpr double kMemLatencyUs = 1.2;
+// flight into sustainable bandwidth, and the fraction of the HBM peak a streaming kernel
+// sustains on MI355X (a device-to-device copy reaches 5.05-5.37 TB/s of 8 TB/s). Both were
+// calibrated on the device against the row-family variant sweep at 4096 x 4096.
+constexpr double kMemLatencyUs = 2.0;
+constexpr double kStreamEff = 0.72;
 // L2 -> CU feed budget (bytes per clock per CU) and LDS read bandwidth per CU.
 constexpr double kL2BytesPerClkPerCu = 64.0;
 constexpr double kLdsBytesPerClkPerCu = 128.0;
@@ -60,19 +63,18 @@ int waves_by_regs(const Hcs& h, int regs) {
 }
 
 // Streaming time of `bytes` over `grid` workgroups, each keeping `inflight_wg` bytes of loads
-// outstanding, with at most `resident_per_cu` workgroups per CU: rounds of resident
-// workgroups, each round at min(peak, in-flight bytes / latency).
+// outstanding, with at most `resident_per_cu` workgroups per CU (Little's law: sustained
+// bandwidth = bytes in flight / latency, capped at the sustainable peak).
 double stream_us(const Hcs& h, double bytes, int64_t grid, int resident_per_cu, double inflight_wg) {
-  const double peak = hbm_gbps(h) * 1e3;  // bytes per microsecond
+  const double peak = hbm_gbps(h) * 1e3 * kStreamEff;  // bytes per microsecond
   const int64_t slots = int64_t(cus(h)) * std::max(resident_per_cu, 1);
-  const double per_wg = bytes / double(std::max<int64_t>(grid, 1));
-  double t = 0;
-  for (int64_t done = 0; done < grid; done += slots) {
-    const int64_t active = std::min(slots, grid - done);
-    const double bw = std::min(peak, double(active) * inflight_wg / kMemLatencyUs);
-    t += double(active) * per_wg / bw;
-  }
-  return t;
+  const int64_t active = std::min(slots, std::max<int64_t>(grid, 1));
+  const double bw = std::min(peak, double(active) * inflight_wg / kMemLatencyUs);
+  // Workgroups that retire while others load let reads and writes overlap; a grid that fits in
+  // one round of resident workgroups loads everything first and writes everything last.
+  const double rounds = double(std::max<int64_t>(grid, 1)) / double(slots);
+  const double overlap = 1.0 - 0.08 / std::max(rounds, 1.0);
+  return bytes / (bw * overlap);
 }
 
 std::string fmt(const char* f, double a) {
@@ -130,7 +132,6 @@ std::optional<Plan> solve_rows(const Hcs& h, const KmlTree& t, const Shape& s, S
     const double useful = double(s.C) / double(cap);
     const double inflight = double(wg) * v.nv * 16.0 * useful;
     double cost = launch_us(h) + stream_us(h, double(w.bytes), grid, resident, inflight);
-    if (v.tpr > 64) cost += 0.05 * (t.op == OpKind::Softmax ? 2 : 1);  // LDS fold + barrier per reduction
     Cand c;
     c.plan.family = Family::Rows;
     c.plan.variant = i;
@@ -251,38 +252,28 @@ std::optional<Plan> solve_gemm(const Hcs& h, const KmlTree& t, const Shape& s, S
 std::optional<Plan> solve_q8(const Hcs& h, const KmlTree& t, const Shape& s, SolveLog* log, std::string* err) {
   const Workload w = workload_of(t);
   std::vector<Cand> cs;
-  const int64_t nblk = s.K / 32;
+  const int64_t npairs = s.K / 64;
   for (int i = 0; i < kNumQ8Variants; ++i) {
     const Q8Variant v = kQ8Variants[i];
     std::ostringstream key;
-    key << "q8_0:waves=" << v.waves << ",kblocks=" << v.kblocks;
-    if (nblk % v.kblocks != 0) {
-      reject(log, key.str() + " violates (K/32)%kblocks==0");
-      continue;
-    }
-    const int64_t ksplit = nblk / v.kblocks;          // wavefronts per 16 output columns
-    if (ksplit % v.waves != 0 && v.waves % ksplit != 0) {
-      reject(log, key.str() + " violates k-split divisibility by waves per workgroup");
-      continue;
-    }
-    const int64_t col_tiles = (s.N + 15) / 16;
-    const int64_t m_tiles = (s.M + 15) / 16;
-    const int64_t waves_total = col_tiles * ksplit * m_tiles;
-    const int64_t grid = (waves_total + v.waves - 1) / v.waves;
-    const int regs = 96;
-    const int wps = waves_by_regs(h, regs);
+    key << "q8_0:waves=" << v.waves;
+    // Wavefronts beyond K/64 block pairs idle (their partial is zero) but still occupy slots.
+    const double busy = std::min(1.0, double(npairs) / double(v.waves));
+    const int64_t grid = ((s.N + 15) / 16) * ((s.M + 15) / 16);
+    const int wps = waves_by_regs(h, 64);
     const int resident = std::max(1, wps * simds(h) / v.waves);
-    const double inflight = double(v.waves) * v.kblocks * 16 * 34.0;  // a wavefront's weight slice
-    const double cost = launch_us(h) + stream_us(h, double(w.bytes), grid, resident, inflight) +
-                        (ksplit > v.waves ? 0.5 : 0.1);
+    // In flight per workgroup: one block pair of 16 rows per wavefront, two with the unroll.
+    const double inflight = double(v.waves) * busy * 2.0 * 16 * 68.0;
+    const double fold_us = 0.05 * v.waves;  // LDS fold of the split-K partials
+    const double cost = launch_us(h) + stream_us(h, double(w.bytes), grid, resident, inflight) + fold_us;
     Cand c;
     c.plan.family = Family::Q8Gemm;
     c.plan.variant = i;
     c.plan.threads = v.waves * 64;
-    c.plan.split_k = int(ksplit);
+    c.plan.split_k = v.waves;
     c.plan.grid = grid;
     c.plan.key = key.str();
-    c.plan.why = std::to_string(grid) + " workgroups, split-K " + std::to_string(ksplit);
+    c.plan.why = std::to_string(grid) + " workgroups of 16 weight rows, K split " + std::to_string(v.waves) + " ways";
     c.cost = cost;
     cs.push_back(c);
   }
@@ -292,40 +283,59 @@ std::optional<Plan> solve_q8(const Hcs& h, const KmlTree& t, const Shape& s, Sol
 // ---------------------------------------------------------------------------------------
 std::optional<Plan> solve_conv(const Hcs& h, const KmlTree& t, const Shape& s, SolveLog* log, std::string* err) {
   const double peak = h.peak_f32_mfma_tflops > 0 ? h.peak_f32_mfma_tflops : h.flops_gflops * 1e-3 / 16;
-  const double flops = double(workload_of(t).ops);
-  const int64_t Mpix = s.Nb * s.Ho * s.Wo;
+  const double clk = clock_ghz(h) * 1e3;  // clocks per microsecond
+  const int64_t taps = s.Kh * s.Kw;
+  const int64_t strips = (s.Ho * s.Wo + 31) / 32;
+  const int64_t units = s.Nb * strips;          // 32-pixel strips
+  const int64_t oc_tiles = (s.Co + 63) / 64;
+  const int64_t waves_total = units * oc_tiles;
+  const double simd_slots = double(cus(h)) * simds(h);
+  // One wavefront's reduction: two 32x32 tiles per (channel pair, tap); an MFMA 32x32x2 f32
+  // occupies the SIMD for 4096 FLOP at the per-SIMD f32 rate.
+  const double per_simd_flop_clk = peak * 1e12 / (simd_slots * clk * 1e6);
+  const double mfma_cycles = 4096.0 / per_simd_flop_clk;
+  const double wave_cycles = 2.0 * double((s.Ci + 1) / 2) * double(taps) * mfma_cycles;
   std::vector<Cand> cs;
   for (int i = 0; i < kNumConvVariants; ++i) {
     const ConvVariant v = kConvVariants[i];
     std::ostringstream key;
-    key << "conv_igemm:" << v.bm << "x" << v.bn << "x" << v.bk << ",w" << v.waves;
-    const int64_t tiles = ((Mpix + v.bm - 1) / v.bm) * ((s.Co + v.bn - 1) / v.bn);
-    const int64_t lds = int64_t(v.bm + v.bn) * v.bk * 4 * 2;
-    if (lds > lds_block(h)) {
-      reject(log, key.str() + " violates LDS");
+    key << "conv_igemm:w" << v.waves << ",lds" << v.bk_bytes;
+    const int64_t per_channel = taps * 64 * 4;
+    int64_t cb = (v.bk_bytes / per_channel) & ~int64_t(1);
+    if (taps > 49) {
+      reject(log, key.str() + " violates taps<=49 (per-lane tap table)");
       continue;
     }
-    const int resident = std::max(1, std::min(int(lds_cu(h) / lds), 8 * simds(h) / v.waves));
-    const int64_t slots = int64_t(cus(h)) * resident;
-    const int64_t rounds = (tiles + slots - 1) / slots;
-    // MFMA work per workgroup lands on `waves` SIMDs; balance = tiles spread over CUs x SIMDs.
-    const double simd_slots = double(cus(h)) * simds(h);
-    const double waves_total = double(tiles) * v.waves;
-    const double per_simd = std::ceil(waves_total / simd_slots);
-    const double balance = waves_total / (per_simd * simd_slots);
-    const double pad_eff = double(Mpix) / double(((Mpix + v.bm - 1) / v.bm) * v.bm) *
-                           double(s.Co) / double(((s.Co + v.bn - 1) / v.bn) * v.bn);
-    const double cost = launch_us(h) + flops / (peak * 1e6 * 0.7 * balance * pad_eff) + 0.5 * double(rounds > 1);
+    if (cb < 2) {
+      reject(log, key.str() + " violates LDS budget >= 2 channels x taps x 64 oc");
+      continue;
+    }
+    if (v.bk_bytes > lds_block(h)) {
+      reject(log, key.str() + " violates LDS per workgroup");
+      continue;
+    }
+    cb = std::min<int64_t>(cb, (s.Ci + 1) & ~int64_t(1));
+    const int64_t lds = cb * per_channel;
+    const int64_t wgs = ((units + v.waves - 1) / v.waves) * oc_tiles;
+    const int resident = std::max(1, int(std::min<int64_t>(lds_cu(h) / lds, 8 * simds(h) / v.waves)));
+    // Wavefronts spread over CUs (workgroup granularity) and SIMDs; the busiest SIMD sets the time.
+    const int64_t wg_per_cu = (wgs + cus(h) - 1) / cus(h);
+    const double waves_per_simd = std::ceil(double(std::min<int64_t>(wg_per_cu, resident)) * v.waves / simds(h)) *
+                                  std::ceil(double(wg_per_cu) / resident);
+    const int64_t chunks = (s.Ci + cb - 1) / cb;
+    const double stage_us = double(chunks) * (double(lds) / 64.0 / clk + 1.0);  // per-CU L2 feed + latency
+    const double cost = launch_us(h) + waves_per_simd * wave_cycles / (clk * 0.8) + stage_us;
     Cand c;
     c.plan.family = Family::ConvIgemm;
     c.plan.variant = i;
-    c.plan.tile_m = v.bm;
-    c.plan.tile_n = v.bn;
-    c.plan.tile_k = v.bk;
+    c.plan.tile_m = 64;
+    c.plan.tile_n = 32 * v.waves;
+    c.plan.tile_k = int(cb * taps);
     c.plan.threads = v.waves * 64;
-    c.plan.grid = tiles;
+    c.plan.grid = wgs;
     c.plan.key = key.str();
-    c.plan.why = std::to_string(tiles) + " tiles, SIMD balance " + fmt("%.2f", balance);
+    c.plan.why = std::to_string(waves_total) + " wavefronts over " + std::to_string(int64_t(simd_slots)) +
+                 " SIMDs, " + std::to_string(cb) + " channels per staged weight chunk";
     c.cost = cost;
     cs.push_back(c);
   }

@@ -1,8 +1,230 @@
-// Implicit-GEMM conv (placeholder launcher until the kernel lands).
+// conv2d as an implicit GEMM on gfx950 f32 matrix cores, with the channelscale epilogue fused.
+//
+// Replaces the reference's SIMT uk_conv<OCB> / uk_conv_g<OCB> (src/codegen_hip.cpp:337-411)
+// and its separate channelscale program (:2329-2335). GEMM view: rows = output channels,
+// columns = output pixels, reduction k = (input channel, kernel tap):
+//   Y[oc][pix] = scale[oc] * sum_k W[oc][k] * X_im2col[k][pix]
+// computed with v_mfma_f32_32x32x2f32. Weights are the MFMA A operand and pixels the B operand,
+// so each accumulator register holds 32 consecutive pixels of one output channel and the
+// epilogue stores coalesce along the pixel axis of Y.
+//
+// Work split: one wavefront owns 32 output pixels of one image (a plane of Ho*Wo pixels is cut
+// into 32-pixel strips) and 64 output channels (two 32x32 tiles); a workgroup is WAVES strips.
+// The weights of one channel chunk ([cb channels][taps][64 oc] floats) are staged once per
+// workgroup in LDS with coalesced reads of the weight rows. The input is gathered straight
+// from global memory with the reduction ordered channel-outer / tap-inner, so the taps of one
+// channel pair re-read the same few cache lines from L1; the next channel pair's gathers are
+// issued before the current pair's MFMAs. Padding taps read as zero.
+//
+// Layouts: NCHW (X[N][C][H][W], W[Oc][C][Kh][Kw], Y[N][Oc][Ho][Wo], zero padding, stride) and
+// the reference's NT conv (X[H][W][C], Wt[Oc][Kh][Kw][C], Y[Oc][Ho][Wo], valid padding,
+// src/reference.cpp:6-22).
 #include "../launch.hpp"
-namespace uk {
-hipError_t launch_conv_igemm(const Plan&, const Shape&, Layout, const float*, const float*, const float*, float*,
-                             hipStream_t) {
-  return hipErrorNotSupported;
+#include "../variants.hpp"
+#include "common.hpp"
+
+namespace uk::kern {
+
+struct ConvArgs {
+  const float* x;
+  const float* w;
+  const float* scale;
+  float* y;
+  int N, C, H, W, Oc, Kh, Kw, pad, stride, Ho, Wo;
+  int strips;  // 32-pixel strips per image
+  int cb;      // channels per staged weight chunk (even)
+};
+
+// Weight index of (oc, c, tap) in the caller's layout.
+template <bool NCHW>
+__device__ __forceinline__ int64_t widx(const ConvArgs& a, int oc, int c, int t) {
+  const int taps = a.Kh * a.Kw;
+  if constexpr (NCHW) return ((int64_t)oc * a.C + c) * taps + t;  // OIHW
+  else return ((int64_t)oc * taps + t) * a.C + c;                 // [Oc][Kh][Kw][C]
 }
+
+template <bool NCHW, int TAPS, int WAVES>
+__global__ void __launch_bounds__(WAVES * 64)
+    conv_igemm_kernel(ConvArgs a) {
+  extern __shared__ float wl[];  // [cb][taps][64]
+  constexpr int kMaxTaps = TAPS > 0 ? TAPS : 49;
+  const int taps = TAPS > 0 ? TAPS : a.Kh * a.Kw;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int unit = blockIdx.x * WAVES + wave;
+  const bool active = unit < a.N * a.strips;
+  const int n = active ? unit / a.strips : 0;
+  const int P = a.Ho * a.Wo;
+  const int p = (active ? unit % a.strips : 0) * 32 + (lane & 31);
+  const bool pvalid = active && p < P;
+  const int ho = pvalid ? p / a.Wo : 0, wo = pvalid ? p % a.Wo : 0;
+  const int kk = lane >> 5;  // k parity within an MFMA k-step: channel c + kk
+  const int oc0 = blockIdx.y * 64;
+
+  // Per-lane input offset of every tap (-1: the tap reads padding).
+  int off[kMaxTaps];
+#pragma unroll
+  for (int t = 0; t < kMaxTaps; ++t) {
+    if (t >= taps) {
+      off[t] = -1;
+      continue;
+    }
+    const int kh = t / a.Kw, kw = t % a.Kw;
+    const int hi = ho * a.stride + kh - a.pad, wi = wo * a.stride + kw - a.pad;
+    const bool ok = pvalid && hi >= 0 && hi < a.H && wi >= 0 && wi < a.W;
+    off[t] = ok ? (NCHW ? hi * a.W + wi : (hi * a.W + wi) * a.C) : -1;
+  }
+  const int64_t HW = (int64_t)a.H * a.W;
+  const float* xb = NCHW ? a.x + (int64_t)n * a.C * HW : a.x;
+  const int64_t cstride = NCHW ? HW : 1;  // distance between channels
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) acc[j][0] = acc[j][1] = f32x16{};
+
+  for (int c0 = 0; c0 < a.C; c0 += a.cb) {
+    const int cn = (a.C - c0) < a.cb ? (a.C - c0) : a.cb;
+    __syncthreads();  // the previous chunk's weight reads are done
+    // Stage W[oc0 .. oc0+63][c0 .. c0+cn)[taps] as wl[c][t][oc]; the inner source index runs
+    // along the contiguous (c, t) or (t, c) run of one weight row.
+    const int per_oc = a.cb * taps;
+    for (int e = threadIdx.x; e < 64 * per_oc; e += WAVES * 64) {
+      const int o = e / per_oc, r = e % per_oc;
+      int cl, t;
+      if constexpr (NCHW) {
+        cl = r / taps;
+        t = r % taps;
+      } else {
+        t = r / a.cb;
+        cl = r % a.cb;
+      }
+      float v = 0.f;
+      if (oc0 + o < a.Oc && cl < cn) v = a.w[widx<NCHW>(a, oc0 + o, c0 + cl, t)];
+      wl[(cl * taps + t) * 64 + o] = v;
+    }
+    __syncthreads();
+
+    // Reduction over this chunk: channel pairs (c, c+1) outer, taps inner.
+    float xv[kMaxTaps], xn[kMaxTaps];
+    auto gather = [&](float (&dst)[kMaxTaps], int c) {
+      const int cc = c + kk;
+      const bool cok = cc < cn;
+      const float* base = xb + (int64_t)(c0 + (cok ? cc : 0)) * cstride;
+#pragma unroll
+      for (int t = 0; t < kMaxTaps; ++t) {
+        const int o = off[t];
+        dst[t] = (t < taps && cok && o >= 0) ? base[o] : 0.f;
+      }
+    };
+    gather(xv, 0);
+    for (int c = 0; c < cn; c += 2) {
+      if (c + 2 < cn) gather(xn, c + 2);
+      const int par = (c >> 1) & 1;
+#pragma unroll
+      for (int t = 0; t < kMaxTaps; ++t) {
+        if (t < taps) {
+          const float* wr = wl + ((c + kk) * taps + t) * 64 + (lane & 31);
+          const float w0 = wr[0], w1 = wr[32];
+          if (par == 0) {
+            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(w0, xv[t], acc[0][0], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(w1, xv[t], acc[1][0], 0, 0, 0);
+          } else {
+            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(w0, xv[t], acc[0][1], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(w1, xv[t], acc[1][1], 0, 0, 0);
+          }
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < kMaxTaps; ++t) xv[t] = xn[t];
+    }
+  }
+
+  // Epilogue: lane -> pixel p (column), rows oc = oc0 + j*32 + 8*(r/4) + 4*(lane>>5) + r%4.
+  if (!pvalid) return;
+  float* yb = NCHW ? a.y + (int64_t)n * a.Oc * P : a.y;
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int oc = oc0 + j * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+      if (oc < a.Oc) {
+        const float s = acc[j][0][r] + acc[j][1][r];
+        yb[(int64_t)oc * P + p] = a.scale ? s * a.scale[oc] : s;
+      }
+    }
+}
+
+}  // namespace uk::kern
+
+namespace uk {
+
+namespace {
+template <bool NCHW, int TAPS, int WAVES>
+hipError_t conv_go(const kern::ConvArgs& a, int64_t units, int oc_tiles, size_t lds, hipStream_t s) {
+  const unsigned grid = (unsigned)((units + WAVES - 1) / WAVES);
+  // Dynamic LDS above the default limit must be requested per kernel (once).
+  static hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&kern::conv_igemm_kernel<NCHW, TAPS, WAVES>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, 163840);
+  if (attr != hipSuccess) return attr;
+  hipLaunchKernelGGL((kern::conv_igemm_kernel<NCHW, TAPS, WAVES>), dim3(grid, (unsigned)oc_tiles), dim3(WAVES * 64),
+                     lds, s, a);
+  return hipGetLastError();
+}
+
+template <bool NCHW, int WAVES>
+hipError_t conv_taps(const kern::ConvArgs& a, int64_t units, int oc_tiles, size_t lds, hipStream_t s) {
+  const int taps = a.Kh * a.Kw;
+  if (taps == 9) return conv_go<NCHW, 9, WAVES>(a, units, oc_tiles, lds, s);
+  if (taps == 1) return conv_go<NCHW, 1, WAVES>(a, units, oc_tiles, lds, s);
+  return conv_go<NCHW, 0, WAVES>(a, units, oc_tiles, lds, s);
+}
+}  // namespace
+
+hipError_t launch_conv_igemm(const Plan& p, const Shape& sh, Layout lay, const float* X, const float* Wt,
+                             const float* scale, float* Y, hipStream_t s) {
+  if (p.family != Family::ConvIgemm || p.variant < 0 || p.variant >= kNumConvVariants) return hipErrorInvalidValue;
+  const ConvVariant v = kConvVariants[p.variant];
+  const bool nchw = lay == Layout::NCHW;
+  if (!nchw && lay != Layout::NT) return hipErrorInvalidValue;
+  if (sh.Ho <= 0 || sh.Wo <= 0 || sh.Ci <= 0 || sh.Co <= 0 || sh.Kh <= 0 || sh.Kw <= 0) return hipErrorInvalidValue;
+  const int64_t taps = sh.Kh * sh.Kw;
+  if (taps > 49) return hipErrorInvalidValue;  // per-lane tap table
+  // Input offsets and plane sizes are 32-bit inside the kernel.
+  if (sh.H * sh.W * sh.Ci > INT32_MAX || sh.Ho * sh.Wo > INT32_MAX || sh.Nb * sh.Ci * sh.H * sh.W > (int64_t(1) << 40))
+    return hipErrorInvalidValue;
+  kern::ConvArgs a;
+  a.x = X;
+  a.w = Wt;
+  a.scale = scale;
+  a.y = Y;
+  a.N = (int)sh.Nb;
+  a.C = (int)sh.Ci;
+  a.H = (int)sh.H;
+  a.W = (int)sh.W;
+  a.Oc = (int)sh.Co;
+  a.Kh = (int)sh.Kh;
+  a.Kw = (int)sh.Kw;
+  a.pad = (int)sh.pad;
+  a.stride = (int)sh.stride;
+  a.Ho = (int)sh.Ho;
+  a.Wo = (int)sh.Wo;
+  a.strips = (int)((sh.Ho * sh.Wo + 31) / 32);
+  // Channel chunk: as many (even) channels as the LDS budget of the variant allows.
+  const int64_t per_channel = taps * 64 * 4;
+  int64_t cb = v.bk_bytes / per_channel;
+  cb &= ~int64_t(1);
+  if (cb < 2) return hipErrorInvalidValue;
+  const int64_t cpad = (sh.Ci + 1) & ~int64_t(1);
+  if (cb > cpad) cb = cpad;
+  a.cb = (int)cb;
+  const size_t lds = (size_t)(cb * per_channel);
+  const int64_t units = sh.Nb * a.strips;
+  const int oc_tiles = (int)((sh.Co + 63) / 64);
+  if ((units + v.waves - 1) / v.waves > INT32_MAX || oc_tiles > 65535) return hipErrorInvalidValue;
+  switch (v.waves) {
+    case 2: return nchw ? conv_taps<true, 2>(a, units, oc_tiles, lds, s) : conv_taps<false, 2>(a, units, oc_tiles, lds, s);
+    case 4: return nchw ? conv_taps<true, 4>(a, units, oc_tiles, lds, s) : conv_taps<false, 4>(a, units, oc_tiles, lds, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 }  // namespace uk

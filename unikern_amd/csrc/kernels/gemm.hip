@@ -133,10 +133,14 @@ __global__ void __launch_bounds__(WM* WN * 64, 1)
 #pragma unroll
     for (int j = 0; j < Cfg::kFN; ++j) acc[i][j] = f32x16{};
 
+  // DMA of k-tile t into its ring slot. The tile index is clamped to the last tile, so the
+  // ring is issued without branches: a clamped issue refills a slot nobody reads again.
+  const int KT = K / BK;
   auto issue = [&](int t) {
     char* st = lds + (t % STAGES) * Cfg::kStageBytes;
-    dma_tile<BM, BK, Cfg::kWaves, SWZ>(Ag + (int64_t)t * BK, K, st, wave, lane);
-    dma_tile<BN, BK, Cfg::kWaves, SWZ>(Bg + (int64_t)t * BK, K, st + BM * Cfg::kRowBytes, wave, lane);
+    const int tc = t < KT ? t : KT - 1;
+    dma_tile<BM, BK, Cfg::kWaves, SWZ>(Ag + (int64_t)tc * BK, K, st, wave, lane);
+    dma_tile<BN, BK, Cfg::kWaves, SWZ>(Bg + (int64_t)tc * BK, K, st + BM * Cfg::kRowBytes, wave, lane);
   };
 
   // Fragment registers, double buffered across k-steps (and across k-tiles).
@@ -158,45 +162,58 @@ __global__ void __launch_bounds__(WM* WN * 64, 1)
       b[j] = *reinterpret_cast<const f16x8*>(Bs + r * Cfg::kRowBytes + ((c ^ swz<SWZ, Cfg::kChunks>(r)) << 4));
     }
   };
+  auto mfmas = [&](const f16x8 (&a)[Cfg::kFM], const f16x8 (&b)[Cfg::kFN]) {
+#pragma unroll
+    for (int i = 0; i < Cfg::kFM; ++i)
+#pragma unroll
+      for (int j = 0; j < Cfg::kFN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[j], a[i], acc[i][j], 0, 0, 0);
+  };
+  constexpr int kMfmaPerStep = Cfg::kFM * Cfg::kFN;
+  constexpr int kReadsPerStep = Cfg::kFM + Cfg::kFN;
 
-  const int KT = K / BK;
   // Prologue: tiles 0 .. STAGES-2 in flight; wait for tile 0 only.
 #pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s)
-    if (s < KT) issue(s);
-  if (KT >= STAGES - 1)
-    wait_vmcnt<(STAGES - 2) * Cfg::kInsts>();
-  else
-    wait_vmcnt<0>();
+  for (int s = 0; s < STAGES - 1; ++s) issue(s);
+  wait_vmcnt<(STAGES - 2) * Cfg::kInsts>();
   __syncthreads();
   load_frags(fa[0], fb[0], 0, 0);
 
   for (int kt = 0; kt < KT; ++kt) {
-    // Tile kt+1 must have landed (this wave's DMA) and be visible (everyone's): its first
-    // fragments are prefetched during this iteration. The barrier also retires every read of
-    // tile kt-1, whose slot the DMA below overwrites.
-    if (kt + 1 < KT) {
-      if (kt + STAGES - 2 < KT)
-        wait_vmcnt<(STAGES - 3) * Cfg::kInsts>();
-      else
-        wait_vmcnt<0>();
-    }
+    // Tile kt+1 has landed for this wave (tiles kt+2 .. kt+STAGES-2 may still fly) and, after
+    // the barrier, for every wave; the barrier also retires all reads of tile kt-1, whose
+    // slot the DMA below refills.
+    wait_vmcnt<(STAGES - 3) * Cfg::kInsts>();
     __syncthreads();
-    if (kt + STAGES - 1 < KT) issue(kt + STAGES - 1);
 #pragma unroll
     for (int kk = 0; kk < Cfg::kKK; ++kk) {
       const int cur = kk & 1;
+      // Next k-step's fragments: the rest of this tile, then the first step of tile kt+1
+      // (re-reading tile kt on the last iteration keeps the code branch-free).
       if (kk + 1 < Cfg::kKK)
         load_frags(fa[cur ^ 1], fb[cur ^ 1], kt, kk + 1);
-      else if (kt + 1 < KT)
-        load_frags(fa[cur ^ 1], fb[cur ^ 1], kt + 1, 0);
+      else
+        load_frags(fa[cur ^ 1], fb[cur ^ 1], kt + 1 < KT ? kt + 1 : kt, 0);
+      if (kk == 0) issue(kt + STAGES - 1);
+      mfmas(fa[cur], fb[cur]);
+      // Spread the LDS reads (and on the first step the DMA) between the MFMAs so the matrix
+      // pipe never drains while they issue.
+      if (kk == 0) {
 #pragma unroll
-      for (int i = 0; i < Cfg::kFM; ++i)
+        for (int q = 0; q < Cfg::kInsts; ++q) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // 1 VMEM read (DMA)
+        }
+      }
 #pragma unroll
-        for (int j = 0; j < Cfg::kFN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[cur][j], fa[cur][i], acc[i][j], 0, 0, 0);
+      for (int q = 0; q < kReadsPerStep; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, kMfmaPerStep, 0);
     }
   }
+  wait_vmcnt<0>();  // clamped refills still in flight must land before LDS is reused
   __syncthreads();
 
   // Epilogue. acc[i][j] holds C^T: lane -> row m = i*32 + (lane & 31) of the wave tile and

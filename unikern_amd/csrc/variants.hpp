@@ -32,35 +32,36 @@ constexpr GemmF16Variant kGemmF16Variants[] = {
     {256, 256, 32, 2, 2, 4, 1},
     {256, 256, 32, 2, 2, 4, 2},
     {256, 256, 32, 2, 2, 4, 0},
-    {256, 256, 32, 2, 4, 4, 1},
-    {256, 128, 32, 2, 2, 4, 1},
+    {256, 256, 32, 2, 4, 4, 2},
+    {256, 128, 32, 2, 2, 4, 2},
     {256, 128, 64, 2, 2, 3, 1},
     {128, 128, 64, 2, 2, 3, 1},
-    {128, 128, 32, 2, 2, 4, 1},
+    {128, 128, 32, 2, 2, 4, 2},
 };
 constexpr int kNumGemmF16Variants = sizeof(kGemmF16Variants) / sizeof(kGemmF16Variants[0]);
 
 // Generic MFMA GEMM (any M, N, K; NT or TN; fp16 or fp32 inputs): 64x64 tiles, 4 waves.
 constexpr int kGemmGenericTile = 64;
 
-// Q8_0 skinny GEMM: 16 output columns (weight rows) per wavefront step, split-K.
+// Q8_0 skinny GEMM: a workgroup owns 16 weight rows; its wavefronts split the K blocks.
 struct Q8Variant {
-  int waves, kblocks;  // waves per workgroup, 32-element blocks per wavefront
+  int waves;
 };
-constexpr Q8Variant kQ8Variants[] = {
-    {4, 8}, {4, 16}, {4, 32}, {8, 8}, {8, 16},
-};
+constexpr Q8Variant kQ8Variants[] = {{4}, {8}, {16}};
 constexpr int kNumQ8Variants = sizeof(kQ8Variants) / sizeof(kQ8Variants[0]);
 
-// Implicit-GEMM conv on f32 MFMA (v_mfma_f32_16x16x4_f32): bm output pixels x bn output
-// channels per workgroup, bk reduction slice.
+// Implicit-GEMM conv on f32 MFMA (v_mfma_f32_32x32x2f32): a wavefront owns 32 output pixels x
+// 64 output channels; waves per workgroup, and the LDS budget for one staged weight chunk
+// (channels per chunk = budget / (taps * 64 * 4 B), even).
 struct ConvVariant {
-  int bm, bn, bk, waves;
+  int waves;
+  int bk_bytes;
 };
 constexpr ConvVariant kConvVariants[] = {
-    {64, 64, 16, 4},
-    {128, 64, 16, 4},
-    {32, 64, 16, 2},
+    {4, 147456},
+    {2, 73728},
+    {4, 73728},
+    {2, 36864},
 };
 constexpr int kNumConvVariants = sizeof(kConvVariants) / sizeof(kConvVariants[0]);
 
