@@ -84,26 +84,52 @@ __global__ void __launch_bounds__(WAVES * 64)
   for (int c0 = 0; c0 < a.C; c0 += a.cb) {
     const int cn = (a.C - c0) < a.cb ? (a.C - c0) : a.cb;
     __syncthreads();  // the previous chunk's weight reads are done
-    // Stage W[oc0 .. oc0+63][c0 .. c0+cn)[taps] as wl[c][t][oc]; the inner source index runs
-    // along the contiguous (c, t) or (t, c) run of one weight row.
-    const int per_oc = a.cb * taps;
-    for (int e = threadIdx.x; e < 64 * per_oc; e += WAVES * 64) {
-      const int o = e / per_oc, r = e % per_oc;
-      int cl, t;
-      if constexpr (NCHW) {
-        cl = r / taps;
-        t = r % taps;
-      } else {
-        t = r / a.cb;
-        cl = r % a.cb;
+    // Stage W[oc0 .. oc0+63][c0 .. c0+cn)[taps] as wl[c][t][oc]: lane = output channel, so the
+    // LDS writes are conflict-free; each wavefront walks the chunk's (c, t) elements, 16 loads in
+    // flight at a time. Each lane reads along its own weight row, so the 64 rows' cache lines
+    // are fetched into L1 once and reused across consecutive elements.
+    {
+      const int per_oc = a.cb * taps;
+      const bool ook = oc0 + lane < a.Oc;
+      const int oc = ook ? oc0 + lane : 0;
+      for (int e0 = wave * 16; e0 < per_oc; e0 += WAVES * 16) {
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int e = e0 + j;
+          int cl, t;
+          if constexpr (NCHW) {
+            cl = e / taps;
+            t = e - cl * taps;
+          } else {
+            t = e / a.cb;
+            cl = e - t * a.cb;
+          }
+          const bool ok = ook && e < per_oc && cl < cn;
+          const float val = a.w[ok ? widx<NCHW>(a, oc, c0 + cl, t) : 0];
+          v[j] = ok ? val : 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int e = e0 + j;
+          if (e < per_oc) {
+            int cl, t;
+            if constexpr (NCHW) {
+              cl = e / taps;
+              t = e - cl * taps;
+            } else {
+              t = e / a.cb;
+              cl = e - t * a.cb;
+            }
+            wl[(cl * taps + t) * 64 + lane] = v[j];
+          }
+        }
       }
-      float v = 0.f;
-      if (oc0 + o < a.Oc && cl < cn) v = a.w[widx<NCHW>(a, oc0 + o, c0 + cl, t)];
-      wl[(cl * taps + t) * 64 + o] = v;
     }
     __syncthreads();
 
-    // Reduction over this chunk: channel pairs (c, c+1) outer, taps inner.
+    // Reduction over this chunk: channel pairs (c, c+1) outer, taps inner. Gathers use clamped
+    // addresses (always inside the input) and a select, so no load is predicated.
     float xv[kMaxTaps], xn[kMaxTaps];
     auto gather = [&](float (&dst)[kMaxTaps], int c) {
       const int cc = c + kk;
@@ -112,29 +138,34 @@ __global__ void __launch_bounds__(WAVES * 64)
 #pragma unroll
       for (int t = 0; t < kMaxTaps; ++t) {
         const int o = off[t];
-        dst[t] = (t < taps && cok && o >= 0) ? base[o] : 0.f;
+        const bool ok = t < taps && cok && o >= 0;
+        const float val = base[ok ? o : 0];
+        dst[t] = ok ? val : 0.f;
       }
     };
-    gather(xv, 0);
-    for (int c = 0; c < cn; c += 2) {
-      if (c + 2 < cn) gather(xn, c + 2);
-      const int par = (c >> 1) & 1;
+    auto step = [&](int c, f32x16& acc0, f32x16& acc1) {
 #pragma unroll
       for (int t = 0; t < kMaxTaps; ++t) {
         if (t < taps) {
           const float* wr = wl + ((c + kk) * taps + t) * 64 + (lane & 31);
-          const float w0 = wr[0], w1 = wr[32];
-          if (par == 0) {
-            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(w0, xv[t], acc[0][0], 0, 0, 0);
-            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(w1, xv[t], acc[1][0], 0, 0, 0);
-          } else {
-            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(w0, xv[t], acc[0][1], 0, 0, 0);
-            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(w1, xv[t], acc[1][1], 0, 0, 0);
-          }
+          acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(wr[0], xv[t], acc0, 0, 0, 0);
+          acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(wr[32], xv[t], acc1, 0, 0, 0);
         }
       }
+    };
+    gather(xv, 0);
+    for (int c = 0; c < cn; c += 4) {
+      // pair c into accumulator set 0, pair c+2 into set 1 (independent MFMA chains)
+      gather(xn, c + 2);
+      step(c, acc[0][0], acc[1][0]);
 #pragma unroll
       for (int t = 0; t < kMaxTaps; ++t) xv[t] = xn[t];
+      if (c + 2 < cn) {
+        gather(xn, c + 4);
+        step(c + 2, acc[0][1], acc[1][1]);
+#pragma unroll
+        for (int t = 0; t < kMaxTaps; ++t) xv[t] = xn[t];
+      }
     }
   }
 

@@ -72,36 +72,47 @@ __global__ void __launch_bounds__(WAVES * 64)
 
   f32x4 yacc = f32x4{0.f, 0.f, 0.f, 0.f};
   const f32x4 zero = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 2
-  for (int p = pb; p < pe; ++p) {
-    const uint32_t* pw = reinterpret_cast<const uint32_t*>(wrow + 68 * p);
-    uint32_t a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0;
-    if (rok) {
-      a0 = pw[2 * g];
-      a1 = pw[2 * g + 1];
-      a2 = pw[2 * g + 2];  // dword 8 also carries the odd block's scale (lanes g = 3)
-      b0 = pw[9 + 2 * g];
-      b1 = pw[10 + 2 * g];
-    }
-    f16x8 xa = {}, xb = {};
-    if (mok) {
-      xa = *reinterpret_cast<const f16x8*>(xrow + 64 * p);
-      xb = *reinterpret_cast<const f16x8*>(xrow + 64 * p + 32);
-    }
-    // Even block: quant bytes 2..9 of this lane's 12-byte window; odd block: aligned.
-    const f16x8 qa = q8_to_f16x8(__builtin_amdgcn_alignbyte(a1, a0, 2), __builtin_amdgcn_alignbyte(a2, a1, 2));
-    const f16x8 qb = q8_to_f16x8(b0, b1);
-    const f32x4 s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa, xa, zero, 0, 0, 0);
-    const f32x4 s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qb, xb, zero, 0, 0, 0);
-    // Scales: d_even of row r sits in the low half of a0 in lane r (g = 0); d_odd of row r in
-    // the high half of a2 in lane 48 + r (g = 3). This lane's outputs are rows 4g + {0..3}.
+  // The wavefront's pairs are processed in chunks of kU: all loads of a chunk are issued
+  // before any of its math, so a wavefront keeps kU * 16 rows * 68 B in flight.
+  constexpr int kU = 4;
+  for (int pc = pb; pc < pe; pc += kU) {
+    uint32_t a0[kU], a1[kU], a2[kU], b0[kU], b1[kU];
+    f16x8 xa[kU], xb[kU];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int src = 4 * g + r;
-      const float d0 = half_bits_to_float((uint32_t)__shfl((int)a0, src));
-      const float d1 = half_bits_to_float((uint32_t)__shfl((int)a2, 48 + src) >> 16);
-      yacc[r] = fmaf(d0, s0[r], yacc[r]);
-      yacc[r] = fmaf(d1, s1[r], yacc[r]);
+    for (int u = 0; u < kU; ++u) {
+      const int p = pc + u;
+      const bool ok = rok && p < pe;
+      const uint32_t* pw = reinterpret_cast<const uint32_t*>(wrow + 68 * (ok ? p : 0));
+      a0[u] = pw[2 * g];
+      a1[u] = pw[2 * g + 1];
+      a2[u] = pw[2 * g + 2];  // dword 8 also carries the odd block's scale (lanes g = 3)
+      b0[u] = pw[9 + 2 * g];
+      b1[u] = pw[10 + 2 * g];
+      if (!ok) a0[u] = a1[u] = a2[u] = b0[u] = b1[u] = 0;
+      const bool xok = mok && p < pe;
+      const _Float16* xp = xrow + 64 * (xok ? p : 0);
+      xa[u] = *reinterpret_cast<const f16x8*>(xp);
+      xb[u] = *reinterpret_cast<const f16x8*>(xp + 32);
+      if (!xok) xa[u] = xb[u] = f16x8{};
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      // Even block: quant bytes 2..9 of this lane's 12-byte window; odd block: aligned.
+      const f16x8 qa = q8_to_f16x8(__builtin_amdgcn_alignbyte(a1[u], a0[u], 2),
+                                   __builtin_amdgcn_alignbyte(a2[u], a1[u], 2));
+      const f16x8 qb = q8_to_f16x8(b0[u], b1[u]);
+      const f32x4 s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa, xa[u], zero, 0, 0, 0);
+      const f32x4 s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qb, xb[u], zero, 0, 0, 0);
+      // Scales: d_even of row r sits in the low half of a0 in lane r (g = 0); d_odd of row r in
+      // the high half of a2 in lane 48 + r (g = 3). This lane's outputs are rows 4g + {0..3}.
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int src = 4 * g + r;
+        const float d0 = half_bits_to_float((uint32_t)__shfl((int)a0[u], src));
+        const float d1 = half_bits_to_float((uint32_t)__shfl((int)a2[u], 48 + src) >> 16);
+        yacc[r] = fmaf(d0, s0[r], yacc[r]);
+        yacc[r] = fmaf(d1, s1[r], yacc[r]);
+      }
     }
   }
 
