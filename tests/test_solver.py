@@ -1,0 +1,124 @@
+"""Solver contract (reference src/solver.cpp:141-186 and its tests, tests/acceptance.cpp:467-581):
+a pure function of (hcs, tree) — bitwise-repeatable, deterministic argmin with a canonical-key
+tie-break, predicates that filter candidates with violation records, infeasible termination when
+nothing is left, and HCS constants that flow into the cost. The candidate set and the cost model
+are CDNA4's (compiled kernel variants, LDS/AGPR/wave-quantisation predicates), so the reference's
+RDNA tile picks are not expected here; these tests port the properties.
+"""
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+BASE = json.loads((ROOT / "samples" / "hcs_mi355x.json").read_text())
+
+
+def hcs(**kw) -> str:
+    h = json.loads(json.dumps(BASE))
+    for k, v in kw.items():
+        if k == "vram":
+            h["tiers"][0]["bytes"] = v
+        else:
+            h[k] = v
+    return json.dumps(h)
+
+
+def configs(uk):
+    return [uk.kml_load(p) for p in sorted((ROOT / "samples").glob("kml_*.json"))]
+
+
+def test_solve_is_bitwise_repeatable(uk):
+    for d in configs(uk):
+        first = uk.solve(d)
+        for _ in range(300):
+            s = uk.solve(d)
+            assert (s.key, s.predicted_us, s.feasible, s.family) == (first.key, first.predicted_us, first.feasible,
+                                                                     first.family)
+
+
+def test_every_baseline_config_has_a_plan(uk):
+    fams = {}
+    for d in configs(uk):
+        s = uk.solve(d)
+        assert s.feasible >= 1 and s.predicted_us > 0
+        fams[uk.op_signature(d)] = s.family
+    assert fams["gemm:fp16:4096x4096x4096:TN"] == "gemm_f16_mfma"
+    assert fams["conv:fp32:56x56x64x3x3x64:NCHW:n8:p1:s1:cs"] == "conv_igemm_mfma"
+    assert fams["rmsnorm:fp32:4096x4096"] == "rows"
+    assert all(f == "q8_0_gemm" for k, f in fams.items() if ":q8_0:" in k)
+
+
+def test_capacity_predicate_terminates_infeasible(uk):
+    # R4.4: an empty candidate set ends infeasible with the violation record
+    d = uk.make_desc("gemm", [4096, 4096, 4096], dtype="fp16", layout="TN")
+    with pytest.raises(uk.UnikernError) as e:
+        uk.solve(d, hcs(vram=1 << 20))
+    msg = str(e.value)
+    assert e.value.code == uk.UK_INFEASIBLE
+    assert "working_set<=device_capacity" in msg and "need=100663296" in msg and "cap=1048576" in msg
+    assert uk.solve(d, hcs(vram=100663296)).feasible >= 1  # exactly fitting is feasible
+
+
+def test_lds_predicate_filters_and_records(uk):
+    small = hcs(lds_bytes_per_block=16384, lds_bytes_per_cu=16384)
+    g = uk.solve(uk.make_desc("gemm", [4096, 4096, 4096], dtype="fp16", layout="TN"), small)
+    assert g.family == "gemm_generic_mfma" and "violates LDS" in g.log
+    with pytest.raises(uk.UnikernError) as e:
+        uk.solve(uk.make_desc("conv", [56, 56, 64, 3, 3, 64], layout="NCHW", batch=8, pad=1,
+                              epilogue="channelscale"), small)
+    assert e.value.code == uk.UK_INFEASIBLE and "violates LDS per workgroup" in str(e.value)
+
+
+def test_divisibility_predicate(uk):
+    s = uk.solve(uk.make_desc("gemm", [4096, 4000, 4096], dtype="fp16", layout="TN"))
+    assert s.family == "gemm_generic_mfma" and "violates M%bm==0" in s.log
+    r = uk.solve(uk.make_desc("softmax", [64, 70001]))
+    assert r.family == "rows_stream"
+
+
+def test_hcs_constants_flow_into_cost(uk):
+    # R3.3: an HBM-bound op's predicted time scales with the declared bandwidth
+    d = uk.make_desc("reduce", [4096, 4096])
+    a = uk.solve(d, hcs(hbm_bw_gbps=8000))
+    b = uk.solve(d, hcs(hbm_bw_gbps=4000))
+    launch = BASE["launch_overhead_us"]
+    assert 1.9 < (b.predicted_us - launch) / (a.predicted_us - launch) < 2.1
+    g = uk.make_desc("gemm", [4096, 4096, 4096], dtype="fp16", layout="TN")
+    fast = uk.solve(g, hcs(peak_f16_mfma_tflops=2516.5824))
+    slow = uk.solve(g, hcs(peak_f16_mfma_tflops=1258.2912))
+    assert slow.predicted_us > 1.8 * (fast.predicted_us - launch)
+    assert uk.solve(d, hcs(constants_version=2)).key == a.key
+
+
+def test_argmin_is_deterministic_under_candidate_ties(uk):
+    # Two HCS that differ only in fields the cost does not read give the same pick, and the
+    # pick of a tie group is the smallest canonical key: rows variants with identical predicted
+    # cost (bandwidth-capped) resolve by key, not by table order.
+    d = uk.make_desc("rmsnorm", [4096, 4096])
+    a = uk.solve(d, hcs(device="renamed"))
+    b = uk.solve(d)
+    assert (a.key, a.predicted_us) == (b.key, b.predicted_us)
+    capped = hcs(hbm_bw_gbps=100)  # every candidate hits the same bandwidth cap
+    s = uk.solve(d, capped)
+    assert s.key == min(k for k in _feasible_rows_keys(uk, d, capped))
+
+
+def _feasible_rows_keys(uk, d, h):
+    out = []
+    for tpr, nv in [(64, 1), (64, 2), (64, 4), (64, 8), (64, 16), (128, 4), (128, 8), (256, 1), (256, 2), (256, 4),
+                    (256, 8), (512, 2), (512, 4), (1024, 1), (1024, 2), (1024, 4)]:
+        cap = tpr * nv * 4
+        C = d.dims[1]
+        if C % 4 == 0 and C <= cap and not (cap >= 4 * C and cap > 256):
+            out.append(f"rows:tpr={tpr},nv={nv}")
+    return out
+
+
+def test_calibrated_gemm_pick(uk):
+    # the variant measured fastest at 4096^3 (eight wavefronts, row>>2 swizzle) is the pick
+    s = uk.solve(uk.make_desc("gemm", [4096, 4096, 4096], dtype="fp16", layout="TN"))
+    assert s.key == "gemm_f16:256x256x32,w2x4,s4,z2"
+    assert s.plan.tile_m == 256 and s.plan.threads == 512

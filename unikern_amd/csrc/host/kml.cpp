@@ -167,7 +167,7 @@ void parse_node(const json::Value& v, const std::string& path, KmlTree* t, std::
       }
       if (wide > INT_MAX) {
         bad("dims[" + std::to_string(i) + "]=" + toks[i].text + " exceeds " + std::to_string(INT_MAX) +
-            ", the largest element index the kernels address");
+            ", the largest element index the generated kernels can address");
         values_ok = false;
         continue;
       }
@@ -281,9 +281,12 @@ std::string fmt_eps(float e) {
   return b;
 }
 
-void export_node(std::ostringstream& os, const KmlTree& t, const std::string& ind) {
-  const std::string in = ind + "  ";
-  os << "{\n";
+void export_node(std::ostringstream& os, const KmlTree& t, bool nested) {
+  // Byte layout of the reference export (src/kml_front.cpp:220-244): top-level fields indented
+  // by two spaces, every child (at any depth) and its fields by four, a child list closed by
+  // "]" on the last child's line. Extension fields follow "layout" with the same indentation.
+  const char* in = nested ? "    " : "  ";
+  os << (nested ? "    {" : "{") << "\n";
   os << in << "\"op\": \"" << to_string(t.op) << "\",\n";
   os << in << "\"dtype\": \"" << to_string(t.dtype) << "\",\n";
   os << in << "\"dims\": [";
@@ -293,19 +296,21 @@ void export_node(std::ostringstream& os, const KmlTree& t, const std::string& in
   os << in << "\"tile_n\": " << t.tile_n << ",\n";
   os << in << "\"layout\": \"" << to_string(t.layout) << "\"";
   if (t.op == OpKind::Conv && t.layout == Layout::NCHW)
-    os << ",\n" << in << "\"batch\": " << t.batch << ",\n" << in << "\"pad\": " << t.pad << ",\n"
-       << in << "\"stride\": " << t.stride;
+    os << ",\n" << in << "\"batch\": " << t.batch << ",\n" << in << "\"pad\": " << t.pad << ",\n" << in
+       << "\"stride\": " << t.stride;
   if (t.epilogue != Epilogue::None) os << ",\n" << in << "\"epilogue\": \"" << to_string(t.epilogue) << "\"";
   if (t.has_eps) os << ",\n" << in << "\"eps\": " << fmt_eps(t.eps);
   if (!t.children.empty()) {
     os << ",\n" << in << "\"children\": [";
     for (size_t i = 0; i < t.children.size(); ++i) {
-      os << (i ? "," : "") << "\n" << in << "  ";
-      export_node(os, t.children[i], in + "  ");
+      os << (i ? "," : "") << "\n";
+      export_node(os, t.children[i], true);
     }
-    os << "\n" << in << "]";
+    os << "]\n";
+  } else {
+    os << "\n";
   }
-  os << "\n" << ind << "}";
+  os << (nested ? "    " : "") << "}";
 }
 
 }  // namespace
@@ -333,7 +338,7 @@ std::optional<KmlTree> kml_import(const std::string& text, std::string* err) {
 
 std::string kml_export(const KmlTree& t) {
   std::ostringstream os;
-  export_node(os, t, "");
+  export_node(os, t, false);
   os << "\n";
   return os.str();
 }

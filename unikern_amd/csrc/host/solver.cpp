@@ -198,7 +198,8 @@ std::optional<Plan> solve_gemm(const Hcs& h, const KmlTree& t, const Shape& s, S
       const int64_t slots = int64_t(cus(h)) * resident;
       const int64_t rounds = (tiles + slots - 1) / slots;
       // Per k-tile of one workgroup: MFMA issue cycles on each SIMD, LDS fragment reads and the
-      // L2 feed of the A/B panels; the slowest sets the pace, the others partly overlap it.
+      // L2 feed of the A/B panels bound the pace from below (the model's feasibility check); the
+      // sustained efficiency is the variant's calibrated one, capped by that bound.
       const double cu_flops_per_clk = peak_tflops * 1e12 / (double(cus(h)) * clk * 1e6);
       const int wg_on_cu = int(std::min<int64_t>(resident, (tiles + cus(h) - 1) / cus(h)));
       const double k16 = double(v.bk) / 16.0;
@@ -206,8 +207,8 @@ std::optional<Plan> solve_gemm(const Hcs& h, const KmlTree& t, const Shape& s, S
                               (32768.0 * simds(h) / cu_flops_per_clk);
       const double lds_clk = double(wg_on_cu) * waves * (fm + fn) * 1024.0 * k16 / kLdsBytesPerClkPerCu;
       const double l2_clk = double(wg_on_cu) * double(v.bm + v.bn) * v.bk * 2.0 / kL2BytesPerClkPerCu;
-      const double pace = std::max({mfma_clk, lds_clk, l2_clk}) + 0.25 * (lds_clk + l2_clk);
-      const double eff = mfma_clk / pace;
+      const double bound = mfma_clk / std::max({mfma_clk, lds_clk, l2_clk});
+      const double eff = std::min(bound, v.eff);
       const double tile_flops = 2.0 * v.bm * v.bn * double(s.K);
       const double l2_need = l2_clk;
       // Workgroups resident on one CU share its MFMA pipes: a round lasts as long as the CU
@@ -350,6 +351,19 @@ std::optional<Plan> solve(const Hcs& h, const KmlTree& t, SolveLog* log, std::st
     return std::nullopt;
   }
   const Shape s = shape_of(t);
+  // Capacity predicate (the reference's only one, tile_working_set<=device_capacity,
+  // src/solver.cpp:14-60): every kernel here keeps the operation's whole working set resident,
+  // so it must fit the device tier; an empty candidate set ends infeasible with the record.
+  if (const int64_t cap = h.device_capacity(); cap > 0) {
+    const int64_t need = workload_of(t).bytes;
+    if (need > cap) {
+      const std::string rec = "working_set<=device_capacity need=" + std::to_string(need) +
+                              " cap=" + std::to_string(cap);
+      reject(log, rec);
+      if (err) *err = "infeasible: " + rec;
+      return std::nullopt;
+    }
+  }
   switch (t.op) {
     case OpKind::Gemm:
       if (t.dtype == DType::Q8_0) return solve_q8(h, t, s, log, err);

@@ -24,19 +24,23 @@ constexpr int kReduceThreads = 256;
 
 // f16 MFMA GEMM, layout TN (A[M][K], B stored [N][K]), v_mfma_f32_32x32x16_f16.
 // bm x bn x bk macro tile; wm x wn waves; stages of LDS buffering; swz selects the LDS
-// XOR swizzle (0: row, 1: row >> 1, 2: row >> 2) for the bank geometry.
+// XOR swizzle (0: row, 1: row >> 1, 2: row >> 2) for the bank geometry. eff is the calibrated
+// fraction of the dense f16 MFMA peak the variant sustains when every CU holds a tile (kernel-only
+// median at M = N = K = 4096 on one MI355X); the solver's cost model scales it by wave
+// quantisation for other shapes.
 struct GemmF16Variant {
   int bm, bn, bk, wm, wn, stages, swz;
+  double eff;
 };
 constexpr GemmF16Variant kGemmF16Variants[] = {
-    {256, 256, 32, 2, 2, 4, 1},
-    {256, 256, 32, 2, 2, 4, 2},
-    {256, 256, 32, 2, 2, 4, 0},
-    {256, 256, 32, 2, 4, 4, 2},
-    {256, 128, 32, 2, 2, 4, 2},
-    {256, 128, 64, 2, 2, 3, 1},
-    {128, 128, 64, 2, 2, 3, 1},
-    {128, 128, 32, 2, 2, 4, 2},
+    {256, 256, 32, 2, 2, 4, 1, 0.325},
+    {256, 256, 32, 2, 2, 4, 2, 0.349},
+    {256, 256, 32, 2, 2, 4, 0, 0.333},
+    {256, 256, 32, 2, 4, 4, 2, 0.388},
+    {256, 128, 32, 2, 2, 4, 2, 0.311},
+    {256, 128, 64, 2, 2, 3, 1, 0.307},
+    {128, 128, 64, 2, 2, 3, 1, 0.223},
+    {128, 128, 32, 2, 2, 4, 2, 0.280},
 };
 constexpr int kNumGemmF16Variants = sizeof(kGemmF16Variants) / sizeof(kGemmF16Variants[0]);
 
