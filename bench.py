@@ -186,6 +186,41 @@ def bench_gemm(uk, O, steps: int, warmup: int, stream):
             "frobenius_rel": fro, "verified": fro <= 1e-2, "sets": sets}
 
 
+def bench_gemm_f32(uk, O, steps: int, warmup: int, stream):
+    """f32 GEMM 1024^3, row-major A and B (the reference's samples/kml_gemm.json
+    shape family), on the bounds-checked f32 MFMA path; verified on sampled rows."""
+    M = N = K = 1024
+    A = O.uniform(M * K, SEED + 0, -1.0, 1.0).reshape(M, K)
+    B = O.uniform(K * N, SEED + 1, -1.0, 1.0).reshape(K, N)
+    d = uk.make_desc("gemm", [M, N, K], dtype="fp32", layout="NT")
+    ms, key, cb, sets = _time_op(uk, d, [A, B], M * N * 4, steps, warmup, stream)
+    rows = np.array([0, 1, 511, 1023])
+    Cg = cb.download(np.float32, (M, N))[rows].astype(np.float64)
+    cb.free()
+    R = A[rows].astype(np.float64) @ B.astype(np.float64)
+    bound = K * 2.0 ** -24 * (np.abs(A[rows]).astype(np.float64) @ np.abs(B).astype(np.float64))
+    tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+    return {"workload": "gemm f32 1024^3, A and B row-major (configs[0])", "ms": round(ms, 6),
+            "value": round(tflops, 2), "unit": "TFLOP/s", "frac_peak": round(tflops / F32_PEAK_TFLOPS, 4),
+            "peak": F32_PEAK_TFLOPS, "plan": key, "verified": bool(np.all(np.abs(Cg - R) <= bound)), "sets": sets}
+
+
+def bench_copy(uk, O, steps: int, warmup: int, stream):
+    """channelscale over X[4096][4096] f32: a streaming copy with a multiply, the calibration
+    kernel for the HBM traffic counters (exactly 2 * 64 MiB + 16 KiB per launch)."""
+    X = _host(uk, "uk_fill_normal", L * Cc, SEED + 10, 0.0, 1.0).reshape(L, Cc)
+    S = _host(uk, "uk_fill_uniform", Cc, SEED + 32, 0.5, 1.5)
+    d = uk.make_desc("channelscale", [L, Cc])
+    ms, key, yb, sets = _time_op(uk, d, [X, S], L * Cc * 4, steps, warmup, stream)
+    y = yb.download(np.float32, (L, Cc))
+    yb.free()
+    nbytes = (2 * L * Cc + Cc) * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"workload": "channelscale f32 4096x4096 (streaming copy; traffic-counter calibration)", "ms": round(ms, 6),
+            "value": round(gbs, 1), "unit": "GB/s", "frac_peak": round(gbs / HBM_PEAK_GBS, 4), "peak": HBM_PEAK_GBS,
+            "plan": key, "verified": bool(np.array_equal(y, O.channelscale(X, S))), "sets": sets}
+
+
 def bench_conv(uk, O, steps: int, warmup: int, stream):
     N, C, H, W, Oc = 8, 64, 56, 56, 64
     x = O.normal(N * C * H * W, SEED + 30, 0.0, 1.0).reshape(N, C, H, W)
@@ -302,6 +337,8 @@ def main():
     if not args.no_secondary:
         sec_steps, sec_warm = max(10, args.steps // 2), max(5, args.warmup // 2)
         secondary.append(bench_gemm(uk, O, sec_steps, sec_warm, stream))
+        secondary.append(bench_gemm_f32(uk, O, sec_steps, sec_warm, stream))
+        secondary.append(bench_copy(uk, O, sec_steps, sec_warm, stream))
         secondary.append(bench_conv(uk, O, sec_steps, sec_warm, stream))
         secondary.extend(bench_q8(uk, O, args.steps, args.warmup, stream))
     uk.lib.uk_stream_destroy(stream)
@@ -309,7 +346,8 @@ def main():
     traffic = None
     tfile = ROOT / "profiles" / "traffic.json"
     if tfile.exists():
-        traffic = json.loads(tfile.read_text()).get(dom)
+        entry = json.loads(tfile.read_text()).get(dom)
+        traffic = entry["bytes"] if entry else None
 
     line = {
         "metric": METRIC,
