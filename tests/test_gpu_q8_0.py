@@ -86,11 +86,13 @@ def test_ragged_shapes(gpu, M, N, K):
     assert frob(q8_gpu(gpu, Xh, blocks, N), O.q8_0_gemm(Xh, blocks, N)) <= 1e-5
 
 
-@pytest.mark.parametrize("vi", range(3))
-def test_every_variant(gpu, vi):
+@pytest.mark.parametrize("vi", range(4))
+@pytest.mark.parametrize("K", [2048, 4608])
+def test_every_variant(gpu, vi, K):
+    # K = 4608 (72 block pairs) leaves a partial last round for every variant
     p = gpu.Plan()
     p.family, p.variant = 8, vi
-    M, N, K = 8, 300, 2048
+    M, N = 8, 300
     blocks, _, _ = make_weights(N, K, 5 + vi)
     Xh = O.f16_bits(O.normal(M * K, 6 + vi, 0.0, 1.0)).reshape(M, K)
     assert frob(q8_gpu(gpu, Xh, blocks, N, plan=p), O.q8_0_gemm(Xh, blocks, N)) <= 1e-5
@@ -99,3 +101,15 @@ def test_every_variant(gpu, vi):
 def test_k_not_whole_block_pairs_is_refused(gpu):
     d = gpu.make_desc("gemm", [4, 16, 96], dtype="q8_0", layout="TN")
     assert "K divisible by 64" in gpu.support_gap(d)
+
+
+def test_sixteen_byte_copies_need_aligned_segments(gpu):
+    # variant 0 copies 16-byte units: K must be a multiple of 64 * pairs (256); K = 192 is not
+    p = gpu.Plan()
+    p.family, p.variant = 8, 0
+    blocks, _, _ = make_weights(17, 192, 3)
+    Xh = O.f16_bits(O.normal(3 * 192, 4, 0.0, 1.0)).reshape(3, 192)
+    with pytest.raises(gpu.UnikernError):
+        q8_gpu(gpu, Xh, blocks, 17, plan=p)
+    # the solver never picks it for such K
+    assert gpu.solve(gpu.make_desc("gemm", [3, 17, 192], dtype="q8_0", layout="TN")).key.endswith("vec=1")

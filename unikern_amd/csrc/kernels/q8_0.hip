@@ -11,17 +11,26 @@
 //   y[m][n] = sum_b float(d[n][b]) * (sum_{i<32} q[n][b][i] * x[m][32b+i])
 // i.e. the dequantised weight d*q enters as the exact product of its two factors.
 //
-// Memory path: a block pair is 68 bytes, so every pair starts 4-byte aligned; lanes read the
-// quants of both blocks with aligned dword loads and realign the even block's (2-byte shifted)
-// bytes with a funnel shift. Each lane converts 8 quants to f16 with the 1024-bias trick
-// (0x6400 | (q ^ 0x80) is the binary16 value 1024 + q + 128; subtracting 1152 is exact). The
-// scales of the 16 rows arrive in lanes 0-15 (even block) and 48-63 (odd block) as a side
-// effect of those loads and are moved to the lanes that hold each row's outputs with ds_bpermute.
+// Memory path: a workgroup owns 16 consecutive weight rows. Each wavefront owns P consecutive
+// block pairs (68 bytes per row) of those rows per round; for one row they are P * 68 contiguous
+// bytes. It copies them into its own LDS area as [row][17 P dwords] with direct-to-LDS DMA of VEC
+// dwords per lane (global_load_lds_dword, or global_load_lds_dwordx4 when every segment is 16-byte
+// aligned: K a multiple of 64 P, P a multiple of 4), activation loads and copies all issued
+// before one wait.
+// No workgroup barrier is needed until the final fold; other wavefronts of the SIMD overlap it.
+// From LDS, lane (i = row, g) reads the quants of both blocks of a pair with five dword reads and
+// realigns the even block's (2-byte shifted) bytes with a funnel shift. Each lane converts 8
+// quants to f16 with the 1024-bias trick (0x6400 | (q ^ 0x80) is the binary16 value 1024 + q +
+// 128; subtracting 1152 is exact). The scales of the 16 rows arrive in lanes 0-15 (even block) and
+// 48-63 (odd block) as a side effect of those reads and are moved to the lanes that hold each
+// row's outputs with ds_bpermute.
 //
 // K must be a multiple of 64 (whole block pairs per row).
-// Work split: a workgroup owns 16 weight rows (and 16 activation rows per grid.y); its WAVES
-// wavefronts split the K blocks and fold their 16x16 partials in LDS in wavefront order
-// (deterministic). Rows past N and activation rows past M are masked, never read.
+// Work split: grid.x = 16-row groups of weights, grid.y = 16-row groups of activations. A round
+// covers WAVES * P pairs; wavefront w takes pairs [w * P, w * P + P) of it. Each wavefront
+// accumulates in registers across rounds; the partials fold in LDS in wavefront order
+// (deterministic). Weight rows past N read row n0 (valid memory) and are never stored;
+// activation rows past M read as zero; pairs past K/64 are copied from pair 0 and skipped.
 #include "../launch.hpp"
 #include "../variants.hpp"
 #include "common.hpp"
@@ -29,6 +38,7 @@
 namespace uk::kern {
 
 typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void;
 
 // Four int8 quants packed in a dword -> four binary16 values (exact).
 __device__ __forceinline__ u32x2 q4_to_f16(uint32_t dw) {
@@ -50,82 +60,120 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xffffu));
 }
 
-template <int WAVES>
+// s_waitcnt vmcnt(N), other counters unconstrained (gfx9 encoding: vmcnt bits 3:0 and 15:14).
+template <int N>
+__device__ __forceinline__ void q8_wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int WAVES, int P, int VEC>
 __global__ void __launch_bounds__(WAVES * 64)
     q8_0_gemm_kernel(const _Float16* __restrict__ X, const uint8_t* __restrict__ Wq, float* __restrict__ Y, int M,
                      int N, int K) {
-  __shared__ float red[WAVES][256];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  static_assert(VEC == 1 || (VEC == 4 && P % 4 == 0), "16-byte copies need 16-byte aligned segments");
+  constexpr int kRowDw = 17 * P;                   // one row's P block pairs, in dwords
+  constexpr int kWaveDw = 16 * kRowDw;             // this wavefront's staging area
+  constexpr int kUnits = kWaveDw / VEC;            // copy units of VEC dwords
+  constexpr int kInst = (kUnits + 63) / 64;        // DMA instructions per round
+  static_assert(2 * P + kInst <= 63, "a round's loads must fit the vmcnt counter");
+  static_assert(WAVES * kWaveDw >= WAVES * 256, "the partials fold reuses the staging buffer");
+  __shared__ uint32_t wl[WAVES * kWaveDw];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
   const int i = lane & 15, g = lane >> 4;
   const int n0 = blockIdx.x * 16, m0 = blockIdx.y * 16;
-  const int nblk = K >> 5, npairs = nblk >> 1;
-  const int per = (npairs + WAVES - 1) / WAVES;
-  const int pb = wave * per;
-  const int pe = (pb + per) < npairs ? (pb + per) : npairs;
+  const int npairs = K >> 6;
+  const int64_t row_bytes = (int64_t)npairs * 68;
+  uint32_t* mine = wl + wave * kWaveDw;
 
-  const int row = n0 + i;
-  const bool rok = row < N;
-  const uint8_t* wrow = Wq + (int64_t)(rok ? row : 0) * nblk * 34;
+  // DMA lane geometry (the same for every round): unit u = t * 64 + lane starts at flattened
+  // dword f = VEC u of the [row][17 P] image, dword d of row r's segment, i.e. dword d % 17 of
+  // its pair d / 17. (With VEC = 4 a unit may straddle two pairs of the segment; the segment is
+  // contiguous in the weight stream, so the copy is still of consecutive bytes.)
+  int src_row[kInst], src_pair[kInst], src_dw[kInst];
+#pragma unroll
+  for (int t = 0; t < kInst; ++t) {
+    const int u = t * 64 + lane;
+    const int f = u * VEC;
+    const int r = f / kRowDw, d = f - (f / kRowDw) * kRowDw;
+    src_row[t] = (u < kUnits && n0 + r < N) ? n0 + r : n0;
+    src_pair[t] = u < kUnits ? d / 17 : 0;
+    src_dw[t] = u < kUnits ? d - (d / 17) * 17 : 0;
+  }
+
   const int m = m0 + i;
   const bool mok = m < M;
   const _Float16* xrow = X + (int64_t)(mok ? m : 0) * K + 8 * g;
+  const uint32_t* lrow = mine + i * kRowDw;
 
   f32x4 yacc = f32x4{0.f, 0.f, 0.f, 0.f};
   const f32x4 zero = f32x4{0.f, 0.f, 0.f, 0.f};
-  // The wavefront's pairs are processed in chunks of kU: all loads of a chunk are issued
-  // before any of its math, so a wavefront keeps kU * 16 rows * 68 B in flight.
-  constexpr int kU = 4;
-  for (int pc = pb; pc < pe; pc += kU) {
-    uint32_t a0[kU], a1[kU], a2[kU], b0[kU], b1[kU];
-    f16x8 xa[kU], xb[kU];
+  for (int base = 0; base < npairs; base += WAVES * P) {
+    const int p0 = base + wave * P;
+    if (p0 >= npairs) break;  // wave-uniform: nothing of this round is ours
+    // Activations of this wavefront's pairs, then the weight copies, then one wait.
+    f16x8 xa[P], xb[P];
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const int p = pc + u;
-      const bool ok = rok && p < pe;
-      const uint32_t* pw = reinterpret_cast<const uint32_t*>(wrow + 68 * (ok ? p : 0));
-      a0[u] = pw[2 * g];
-      a1[u] = pw[2 * g + 1];
-      a2[u] = pw[2 * g + 2];  // dword 8 also carries the odd block's scale (lanes g = 3)
-      b0[u] = pw[9 + 2 * g];
-      b1[u] = pw[10 + 2 * g];
-      if (!ok) a0[u] = a1[u] = a2[u] = b0[u] = b1[u] = 0;
-      const bool xok = mok && p < pe;
-      const _Float16* xp = xrow + 64 * (xok ? p : 0);
-      xa[u] = *reinterpret_cast<const f16x8*>(xp);
-      xb[u] = *reinterpret_cast<const f16x8*>(xp + 32);
-      if (!xok) xa[u] = xb[u] = f16x8{};
+    for (int j = 0; j < P; ++j) {
+      const int p = p0 + j;
+      const _Float16* xp = xrow + 64 * (p < npairs ? p : 0);
+      xa[j] = *reinterpret_cast<const f16x8*>(xp);
+      xb[j] = *reinterpret_cast<const f16x8*>(xp + 32);
     }
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
+    for (int t = 0; t < kInst; ++t) {
+      const int p = p0 + src_pair[t];
+      const uint32_t* src = reinterpret_cast<const uint32_t*>(Wq + (int64_t)src_row[t] * row_bytes +
+                                                              (int64_t)(p < npairs ? p : 0) * 68) + src_dw[t];
+      lds_void* dst = (lds_void*)(mine + t * 64 * VEC);
+      if (t * 64 + lane < kUnits) {
+        if constexpr (VEC == 4) __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+        else __builtin_amdgcn_global_load_lds(src, dst, 4, 0, 0);
+      }
+    }
+    q8_wait_vmcnt<0>();
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+      const int p = p0 + j;
+      if (p >= npairs) break;  // wave-uniform: the round's tail
+      const uint32_t* pw = lrow + 17 * j;
+      const uint32_t a0 = pw[2 * g], a1 = pw[2 * g + 1];
+      const uint32_t a2 = pw[2 * g + 2];  // dword 8 also carries the odd block's scale (lanes g = 3)
+      const uint32_t b0 = pw[9 + 2 * g], b1 = pw[10 + 2 * g];
+      const f16x8 x0 = mok ? xa[j] : f16x8{};
+      const f16x8 x1 = mok ? xb[j] : f16x8{};
       // Even block: quant bytes 2..9 of this lane's 12-byte window; odd block: aligned.
-      const f16x8 qa = q8_to_f16x8(__builtin_amdgcn_alignbyte(a1[u], a0[u], 2),
-                                   __builtin_amdgcn_alignbyte(a2[u], a1[u], 2));
-      const f16x8 qb = q8_to_f16x8(b0[u], b1[u]);
-      const f32x4 s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa, xa[u], zero, 0, 0, 0);
-      const f32x4 s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qb, xb[u], zero, 0, 0, 0);
+      const f16x8 qa = q8_to_f16x8(__builtin_amdgcn_alignbyte(a1, a0, 2), __builtin_amdgcn_alignbyte(a2, a1, 2));
+      const f16x8 qb = q8_to_f16x8(b0, b1);
+      const f32x4 s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa, x0, zero, 0, 0, 0);
+      const f32x4 s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qb, x1, zero, 0, 0, 0);
       // Scales: d_even of row r sits in the low half of a0 in lane r (g = 0); d_odd of row r in
-      // the high half of a2 in lane 48 + r (g = 3). This lane's outputs are rows 4g + {0..3}.
+      // the high half of a2 in lane 48 + r (g = 3). This lane's outputs are rows 4g + 0..3.
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int src = 4 * g + r;
-        const float d0 = half_bits_to_float((uint32_t)__shfl((int)a0[u], src));
-        const float d1 = half_bits_to_float((uint32_t)__shfl((int)a2[u], 48 + src) >> 16);
+        const float d0 = half_bits_to_float((uint32_t)__shfl((int)a0, src));
+        const float d1 = half_bits_to_float((uint32_t)__shfl((int)a2, 48 + src) >> 16);
         yacc[r] = fmaf(d0, s0[r], yacc[r]);
         yacc[r] = fmaf(d1, s1[r], yacc[r]);
       }
     }
   }
 
-  // Fold the wavefronts' partials in wavefront order.
+  // Fold the wavefronts' partials in wavefront order (in the staging buffer, once every
+  // wavefront is done reading it).
+  float* red = reinterpret_cast<float*>(wl);
+  __syncthreads();
 #pragma unroll
-  for (int r = 0; r < 4; ++r) red[wave][lane * 4 + r] = yacc[r];
+  for (int r = 0; r < 4; ++r) red[wave * 256 + lane * 4 + r] = yacc[r];
   __syncthreads();
   if (wave != 0) return;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    float s = red[0][lane * 4 + r];
+    float s = red[lane * 4 + r];
 #pragma unroll
-    for (int w = 1; w < WAVES; ++w) s += red[w][lane * 4 + r];
+    for (int w = 1; w < WAVES; ++w) s += red[w * 256 + lane * 4 + r];
     const int n = n0 + 4 * g + r;  // MFMA output row = weight row
     if (n < N && mok) Y[(int64_t)m * N + n] = s;
   }
@@ -136,11 +184,11 @@ __global__ void __launch_bounds__(WAVES * 64)
 namespace uk {
 
 namespace {
-template <int WAVES>
+template <int WAVES, int P, int VEC>
 hipError_t q8_go(const void* X, const void* Wq, float* Y, int64_t M, int64_t N, int64_t K, hipStream_t s) {
   const dim3 grid((unsigned)((N + 15) / 16), (unsigned)((M + 15) / 16));
-  hipLaunchKernelGGL((kern::q8_0_gemm_kernel<WAVES>), grid, dim3(WAVES * 64), 0, s, static_cast<const _Float16*>(X),
-                     static_cast<const uint8_t*>(Wq), Y, (int)M, (int)N, (int)K);
+  hipLaunchKernelGGL((kern::q8_0_gemm_kernel<WAVES, P, VEC>), grid, dim3(WAVES * 64), 0, s,
+                     static_cast<const _Float16*>(X), static_cast<const uint8_t*>(Wq), Y, (int)M, (int)N, (int)K);
   return hipGetLastError();
 }
 }  // namespace
@@ -150,17 +198,24 @@ hipError_t launch_q8_gemm(const Plan& p, const void* X, const void* Wq, float* Y
   if (p.family != Family::Q8Gemm || p.variant < 0 || p.variant >= kNumQ8Variants) return hipErrorInvalidValue;
   // Whole block pairs per row keep every row (34*K/32 bytes) and pair 4-byte aligned.
   if (M <= 0 || N <= 0 || K <= 0 || K % 64) return hipErrorInvalidValue;
-  // Row byte offsets and element indices are formed in 32/64-bit as above; grid limits.
-  if ((N + 15) / 16 > INT32_MAX || (M + 15) / 16 > 65535 || K > INT32_MAX / 2 || N > INT32_MAX) return hipErrorInvalidValue;
-  // Activation rows are read as 16-byte vectors at 2*(m*K + 32b + 8g) bytes; rows of the weight
-  // stream are 34*K/32 bytes, pairs 68 bytes: both need 4-byte alignment, X 16-byte.
+  // Row byte offsets are 64-bit, element indices 32-bit; grid limits.
+  if ((N + 15) / 16 > INT32_MAX || (M + 15) / 16 > 65535 || K > INT32_MAX / 2 || N > INT32_MAX ||
+      M * K > INT32_MAX)
+    return hipErrorInvalidValue;
+  // Activation rows are read as 16-byte vectors at 2*(m*K + 64p + 8g [+ 32]) bytes (16-byte
+  // aligned when X is); the weight stream is copied as dwords (4-byte aligned rows and pairs).
   if ((((uintptr_t)X) & 15) || (((uintptr_t)Wq) & 3) || (((uintptr_t)Y) & 3)) return hipErrorInvalidValue;
-  switch (kQ8Variants[p.variant].waves) {
-    case 4: return q8_go<4>(X, Wq, Y, M, N, K, s);
-    case 8: return q8_go<8>(X, Wq, Y, M, N, K, s);
-    case 16: return q8_go<16>(X, Wq, Y, M, N, K, s);
-    default: return hipErrorInvalidValue;
-  }
+  const Q8Variant v = kQ8Variants[p.variant];
+  // 16-byte copies: every wavefront segment (64 P elements of K) starts 16-byte aligned.
+  if (v.vec == 4 && ((K % (64 * v.pairs)) != 0 || (((uintptr_t)Wq) & 15))) return hipErrorInvalidValue;
+#define UK_Q8_CASE(W, PV, VV) \
+  if (v.waves == W && v.pairs == PV && v.vec == VV) return q8_go<W, PV, VV>(X, Wq, Y, M, N, K, s);
+  UK_Q8_CASE(16, 4, 4)
+  UK_Q8_CASE(16, 4, 1)
+  UK_Q8_CASE(8, 8, 4)
+  UK_Q8_CASE(8, 4, 1)
+#undef UK_Q8_CASE
+  return hipErrorInvalidValue;
 }
 
 }  // namespace uk

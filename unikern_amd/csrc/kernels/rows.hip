@@ -20,7 +20,19 @@
 
 namespace uk::kern {
 
-template <int TPR, int NV, int OP>
+// Loads and stores of the row stream; NT adds the non-temporal hint.
+template <bool NT>
+__device__ __forceinline__ f32x4 ld4(const f32x4* p) {
+  if constexpr (NT) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+template <bool NT>
+__device__ __forceinline__ void st4(f32x4* p, f32x4 v) {
+  if constexpr (NT) __builtin_nontemporal_store(v, p);
+  else *p = v;
+}
+
+template <int TPR, int NV, int OP, bool NT>
 __global__ void __launch_bounds__(TPR < 256 ? 256 : TPR)
     rows_kernel(const float* __restrict__ X, const float* __restrict__ Wg, float* __restrict__ Y, int L, int C,
                 float eps) {
@@ -45,7 +57,7 @@ __global__ void __launch_bounds__(TPR < 256 ? 256 : TPR)
   for (int i = 0; i < NV; ++i) {
     const int j = i * TPR + t;
     if (active && j < C4) {
-      v[i] = x4[j];
+      v[i] = ld4<NT>(x4 + j);
     } else {
       v[i] = f32x4{fill, fill, fill, fill};
     }
@@ -113,7 +125,7 @@ __global__ void __launch_bounds__(TPR < 256 ? 256 : TPR)
           o.y = __fmul_rn(__fmul_rn(v[i].y, rms), g[i].y);
           o.z = __fmul_rn(__fmul_rn(v[i].z, rms), g[i].z);
           o.w = __fmul_rn(__fmul_rn(v[i].w, rms), g[i].w);
-          y4[j] = o;
+          st4<NT>(y4 + j, o);
         }
       }
     }
@@ -137,7 +149,7 @@ __global__ void __launch_bounds__(TPR < 256 ? 256 : TPR)
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
         const int j = i * TPR + t;
-        if (j < C4) y4[j] = f32x4{v[i].x / s, v[i].y / s, v[i].z / s, v[i].w / s};
+        if (j < C4) st4<NT>(y4 + j, f32x4{v[i].x / s, v[i].y / s, v[i].z / s, v[i].w / s});
       }
     }
   }
@@ -259,7 +271,7 @@ __global__ void __launch_bounds__(kReduceThreads)
 namespace uk {
 
 namespace {
-template <int TPR, int NV>
+template <int TPR, int NV, bool NT>
 hipError_t rows_dispatch_op(RowOp op, const float* X, const float* W, float* Y, int64_t L, int64_t C, float eps,
                             hipStream_t s) {
   constexpr int WG = TPR < 256 ? 256 : TPR;
@@ -267,15 +279,15 @@ hipError_t rows_dispatch_op(RowOp op, const float* X, const float* W, float* Y, 
   const int64_t grid = (L + RPW - 1) / RPW;
   switch (op) {
     case RowOp::Sum:
-      hipLaunchKernelGGL((kern::rows_kernel<TPR, NV, 0>), dim3((unsigned)grid), dim3(WG), 0, s, X, W, Y, (int)L,
+      hipLaunchKernelGGL((kern::rows_kernel<TPR, NV, 0, NT>), dim3((unsigned)grid), dim3(WG), 0, s, X, W, Y, (int)L,
                          (int)C, eps);
       break;
     case RowOp::RmsNorm:
-      hipLaunchKernelGGL((kern::rows_kernel<TPR, NV, 1>), dim3((unsigned)grid), dim3(WG), 0, s, X, W, Y, (int)L,
+      hipLaunchKernelGGL((kern::rows_kernel<TPR, NV, 1, NT>), dim3((unsigned)grid), dim3(WG), 0, s, X, W, Y, (int)L,
                          (int)C, eps);
       break;
     case RowOp::Softmax:
-      hipLaunchKernelGGL((kern::rows_kernel<TPR, NV, 2>), dim3((unsigned)grid), dim3(WG), 0, s, X, W, Y, (int)L,
+      hipLaunchKernelGGL((kern::rows_kernel<TPR, NV, 2, NT>), dim3((unsigned)grid), dim3(WG), 0, s, X, W, Y, (int)L,
                          (int)C, eps);
       break;
   }
@@ -312,9 +324,10 @@ hipError_t launch_rows(const Plan& p, RowOp op, const float* X, const float* W, 
   if ((C & 3) != 0 || C > (int64_t)v.tpr * v.nv * 4) return hipErrorInvalidValue;
   if ((((uintptr_t)X) & 15) || (((uintptr_t)Y) & 15) || (W && (((uintptr_t)W) & 15))) return hipErrorInvalidValue;
   switch (p.variant) {
+  static_assert(kNumRowsVariants == 21, "every rows variant needs a case below");
 #define UK_ROWS_CASE(I)                                                                                 \
   case I:                                                                                               \
-    return rows_dispatch_op<kRowsVariants[I].tpr, kRowsVariants[I].nv>(op, X, W, Y, L, C, eps, s);
+    return rows_dispatch_op<kRowsVariants[I].tpr, kRowsVariants[I].nv, kRowsVariants[I].nt != 0>(op, X, W, Y, L, C, eps, s);
     UK_ROWS_CASE(0)
     UK_ROWS_CASE(1)
     UK_ROWS_CASE(2)
@@ -331,6 +344,11 @@ hipError_t launch_rows(const Plan& p, RowOp op, const float* X, const float* W, 
     UK_ROWS_CASE(13)
     UK_ROWS_CASE(14)
     UK_ROWS_CASE(15)
+    UK_ROWS_CASE(16)
+    UK_ROWS_CASE(17)
+    UK_ROWS_CASE(18)
+    UK_ROWS_CASE(19)
+    UK_ROWS_CASE(20)
 #undef UK_ROWS_CASE
     default: return hipErrorInvalidValue;
   }

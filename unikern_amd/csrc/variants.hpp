@@ -8,12 +8,15 @@ namespace uk {
 // Row family (row-sum, RMSNorm, softmax with the row held in registers).
 // tpr: threads per row (whole wavefronts), nv: float4 registers per thread.
 // A workgroup is max(tpr, 256) threads, i.e. 256/tpr rows per workgroup when tpr < 256.
+// nt: loads and stores carry the non-temporal hint (streamed data bypasses cache retention).
 struct RowsVariant {
-  int tpr, nv;
+  int tpr, nv, nt;
 };
 constexpr RowsVariant kRowsVariants[] = {
-    {64, 1},   {64, 2},   {64, 4},   {64, 8},  {64, 16}, {128, 4}, {128, 8}, {256, 1},
-    {256, 2},  {256, 4},  {256, 8},  {512, 2}, {512, 4}, {1024, 1}, {1024, 2}, {1024, 4},
+    {64, 1, 0},   {64, 2, 0},   {64, 4, 0},  {64, 8, 0},    {64, 16, 0},   {128, 4, 0},
+    {128, 8, 0},  {256, 1, 0},  {256, 2, 0}, {256, 4, 0},   {256, 8, 0},   {512, 2, 0},
+    {512, 4, 0},  {1024, 1, 0}, {1024, 2, 0}, {1024, 4, 0}, {256, 4, 1},   {512, 2, 1},
+    {1024, 1, 1}, {512, 4, 1},  {1024, 2, 1},
 };
 constexpr int kNumRowsVariants = sizeof(kRowsVariants) / sizeof(kRowsVariants[0]);
 constexpr int kRowsStreamThreads = 256;
@@ -47,11 +50,14 @@ constexpr int kNumGemmF16Variants = sizeof(kGemmF16Variants) / sizeof(kGemmF16Va
 // Generic MFMA GEMM (any M, N, K; NT or TN; fp16 or fp32 inputs): 64x64 tiles, 4 waves.
 constexpr int kGemmGenericTile = 64;
 
-// Q8_0 skinny GEMM: a workgroup owns 16 weight rows; its wavefronts split the K blocks.
+// Q8_0 skinny GEMM: a workgroup owns 16 weight rows; each of its wavefronts copies `pairs`
+// block pairs of those rows per round into its own LDS area (pairs * 1088 bytes) and computes
+// them; a round covers waves * pairs block pairs. vec: dwords per lane per copy instruction
+// (4 needs K divisible by 64 * pairs).
 struct Q8Variant {
-  int waves;
+  int waves, pairs, vec;
 };
-constexpr Q8Variant kQ8Variants[] = {{4}, {8}, {16}};
+constexpr Q8Variant kQ8Variants[] = {{16, 4, 4}, {16, 4, 1}, {8, 8, 4}, {8, 4, 1}};
 constexpr int kNumQ8Variants = sizeof(kQ8Variants) / sizeof(kQ8Variants[0]);
 
 // Implicit-GEMM conv on f32 MFMA (v_mfma_f32_32x32x2f32): a wavefront owns 32 output pixels x
