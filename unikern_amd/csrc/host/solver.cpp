@@ -261,8 +261,8 @@ std::optional<Plan> solve_q8(const Hcs& h, const KmlTree& t, const Shape& s, Sol
   for (int i = 0; i < kNumQ8Variants; ++i) {
     const Q8Variant v = kQ8Variants[i];
     std::ostringstream key;
-    key << "q8_0:waves=" << v.waves << ",pairs=" << v.pairs << ",vec=" << v.vec;
-    const int64_t lds = int64_t(v.waves) * v.pairs * 16 * 17 * 4;
+    key << "q8_0:waves=" << v.waves << ",pairs=" << v.pairs << ",vec=" << v.vec << (v.db ? ",db" : "");
+    const int64_t lds = int64_t(v.waves) * v.pairs * 16 * 17 * 4 * (v.db ? 2 : 1);
     if (v.vec == 4 && s.K % (64 * v.pairs) != 0) {
       reject(log, key.str() + " violates K%(64*pairs)==0 (16-byte aligned copies)");
       continue;
@@ -278,8 +278,8 @@ std::optional<Plan> solve_q8(const Hcs& h, const KmlTree& t, const Shape& s, Sol
     const int64_t grid = ((s.N + 15) / 16) * ((s.M + 15) / 16);
     const int wps = waves_by_regs(h, 96);
     const int resident = std::max(1, std::min<int>(wps * simds(h) / v.waves, int(lds_cu(h) / lds)));
-    // Bytes in flight per workgroup: one round of copies.
-    const double inflight = double(per_round) * 16.0 * 68.0 * useful;
+    // Bytes in flight per workgroup: one round of copies (two with double buffering).
+    const double inflight = double(per_round) * 16.0 * 68.0 * useful * (v.db && rounds > 1 ? 2.0 : 1.0);
     // Copy instructions: 16-byte copies issue a quarter of the dword ones.
     const double issue_us = double(rounds) * (v.vec == 4 ? 0.3 : 1.2);
     const double cost = launch_us(h) + stream_us(h, double(w.bytes) / useful, grid, resident, inflight) + issue_us;

@@ -5,8 +5,8 @@
 // Dequantised value w = float(d) * float(q) is exact in binary32 (11 + 7 significant bits).
 //
 // One v_mfma_f32_16x16x32_f16 covers exactly one block of 16 weight rows against 16 activation
-// rows: A = the block's quants as f16 (integers in [-128, 127] are exact in binary16), B = the
-// matching 32 activations. The MFMA sums q*x with products exact and an f32 accumulator; the
+// rows: A = the matching 32 activations, B = the block's quants as f16 (integers in [-128, 127]
+// are exact in binary16). The MFMA sums q*x with products exact and an f32 accumulator; the
 // block scale then multiplies that block sum in f32 and the result is accumulated in f32:
 //   y[m][n] = sum_b float(d[n][b]) * (sum_{i<32} q[n][b][i] * x[m][32b+i])
 // i.e. the dequantised weight d*q enters as the exact product of its two factors.
@@ -21,9 +21,8 @@
 // From LDS, lane (i = row, g) reads the quants of both blocks of a pair with five dword reads and
 // realigns the even block's (2-byte shifted) bytes with a funnel shift. Each lane converts 8
 // quants to f16 with the 1024-bias trick (0x6400 | (q ^ 0x80) is the binary16 value 1024 + q +
-// 128; subtracting 1152 is exact). The scales of the 16 rows arrive in lanes 0-15 (even block) and
-// 48-63 (odd block) as a side effect of those reads and are moved to the lanes that hold each
-// row's outputs with ds_bpermute.
+// 128; subtracting 1152 is exact). The MFMA takes the activations as A and the quants as B, so a
+// lane's outputs all belong to one weight row and its two block scales are one LDS broadcast.
 //
 // K must be a multiple of 64 (whole block pairs per row).
 // Work split: grid.x = 16-row groups of weights, grid.y = 16-row groups of activations. A round
@@ -40,11 +39,14 @@ namespace uk::kern {
 typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void lds_void;
 
-// Four int8 quants packed in a dword -> four binary16 values (exact).
+// Four int8 quants packed in a dword -> four binary16 values (exact): with u = q ^ 0x80 = q + 128
+// as an unsigned byte, the binary16 pattern 0x64uu is 1024 + u; v_perm_b32 places the bytes
+// under 0x64 high bytes (selector byte 4 picks the first operand's low byte, 0..3 the second's)
+// and one packed subtract of 1152 leaves q.
 __device__ __forceinline__ u32x2 q4_to_f16(uint32_t dw) {
-  const uint32_t u = dw ^ 0x80808080u;  // q + 128 as unsigned bytes
-  const uint32_t lo = (u & 0xffu) | ((u & 0xff00u) << 8) | 0x64006400u;
-  const uint32_t hi = ((u >> 16) & 0xffu) | ((u >> 8) & 0xff0000u) | 0x64006400u;
+  const uint32_t u = dw ^ 0x80808080u;
+  const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+  const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
   const f16x2v bias = {(_Float16)1152.0f, (_Float16)1152.0f};
   const f16x2v l = __builtin_bit_cast(f16x2v, lo) - bias;
   const f16x2v h = __builtin_bit_cast(f16x2v, hi) - bias;
@@ -67,7 +69,7 @@ __device__ __forceinline__ void q8_wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <int WAVES, int P, int VEC>
+template <int WAVES, int P, int VEC, bool DB>
 __global__ void __launch_bounds__(WAVES * 64)
     q8_0_gemm_kernel(const _Float16* __restrict__ X, const uint8_t* __restrict__ Wq, float* __restrict__ Y, int M,
                      int N, int K) {
@@ -76,16 +78,16 @@ __global__ void __launch_bounds__(WAVES * 64)
   constexpr int kWaveDw = 16 * kRowDw;             // this wavefront's staging area
   constexpr int kUnits = kWaveDw / VEC;            // copy units of VEC dwords
   constexpr int kInst = (kUnits + 63) / 64;        // DMA instructions per round
-  static_assert(2 * P + kInst <= 63, "a round's loads must fit the vmcnt counter");
+  static_assert(2 * (2 * P + kInst) <= 63, "two rounds of loads must fit the vmcnt counter");
   static_assert(WAVES * kWaveDw >= WAVES * 256, "the partials fold reuses the staging buffer");
-  __shared__ uint32_t wl[WAVES * kWaveDw];
+  __shared__ uint32_t wl[WAVES * kWaveDw * (DB ? 2 : 1)];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int i = lane & 15, g = lane >> 4;
   const int n0 = blockIdx.x * 16, m0 = blockIdx.y * 16;
   const int npairs = K >> 6;
   const int64_t row_bytes = (int64_t)npairs * 68;
-  uint32_t* mine = wl + wave * kWaveDw;
+  uint32_t* mine = wl + wave * kWaveDw * (DB ? 2 : 1);
 
   // DMA lane geometry (the same for every round): unit u = t * 64 + lane starts at flattened
   // dword f = VEC u of the [row][17 P] image, dword d of row r's segment, i.e. dword d % 17 of
@@ -105,15 +107,13 @@ __global__ void __launch_bounds__(WAVES * 64)
   const int m = m0 + i;
   const bool mok = m < M;
   const _Float16* xrow = X + (int64_t)(mok ? m : 0) * K + 8 * g;
-  const uint32_t* lrow = mine + i * kRowDw;
 
   f32x4 yacc = f32x4{0.f, 0.f, 0.f, 0.f};
   const f32x4 zero = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int base = 0; base < npairs; base += WAVES * P) {
-    const int p0 = base + wave * P;
-    if (p0 >= npairs) break;  // wave-uniform: nothing of this round is ours
-    // Activations of this wavefront's pairs, then the weight copies, then one wait.
-    f16x8 xa[P], xb[P];
+  // Round issue: the activations of this wavefront's pairs p0 .. p0 + P - 1, then the weight
+  // copies into `buf`. Pairs past K/64 read pair 0 (valid memory) and are skipped below.
+  auto issue = [&](int p0, uint32_t* buf, f16x8 (&xa)[P], f16x8 (&xb)[P]) {
+    __asm__ volatile("" ::: "memory");  // the buffer's previous reads stay before its refill
 #pragma unroll
     for (int j = 0; j < P; ++j) {
       const int p = p0 + j;
@@ -126,17 +126,19 @@ __global__ void __launch_bounds__(WAVES * 64)
       const int p = p0 + src_pair[t];
       const uint32_t* src = reinterpret_cast<const uint32_t*>(Wq + (int64_t)src_row[t] * row_bytes +
                                                               (int64_t)(p < npairs ? p : 0) * 68) + src_dw[t];
-      lds_void* dst = (lds_void*)(mine + t * 64 * VEC);
+      lds_void* dst = (lds_void*)(buf + t * 64 * VEC);
       if (t * 64 + lane < kUnits) {
         if constexpr (VEC == 4) __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
         else __builtin_amdgcn_global_load_lds(src, dst, 4, 0, 0);
       }
     }
-    q8_wait_vmcnt<0>();
+  };
+  auto compute = [&](int p0, const uint32_t* buf, const f16x8 (&xa)[P], const f16x8 (&xb)[P]) {
+    const uint32_t* lrow = buf + i * kRowDw;
 #pragma unroll
     for (int j = 0; j < P; ++j) {
       const int p = p0 + j;
-      if (p >= npairs) break;  // wave-uniform: the round's tail
+      if (p >= npairs) break;  // wave-uniform: the last round's tail
       const uint32_t* pw = lrow + 17 * j;
       const uint32_t a0 = pw[2 * g], a1 = pw[2 * g + 1];
       const uint32_t a2 = pw[2 * g + 2];  // dword 8 also carries the odd block's scale (lanes g = 3)
@@ -146,19 +148,56 @@ __global__ void __launch_bounds__(WAVES * 64)
       // Even block: quant bytes 2..9 of this lane's 12-byte window; odd block: aligned.
       const f16x8 qa = q8_to_f16x8(__builtin_amdgcn_alignbyte(a1, a0, 2), __builtin_amdgcn_alignbyte(a2, a1, 2));
       const f16x8 qb = q8_to_f16x8(b0, b1);
-      const f32x4 s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa, x0, zero, 0, 0, 0);
-      const f32x4 s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qb, x1, zero, 0, 0, 0);
-      // Scales: d_even of row r sits in the low half of a0 in lane r (g = 0); d_odd of row r in
-      // the high half of a2 in lane 48 + r (g = 3). This lane's outputs are rows 4g + 0..3.
+      // A = activations (row m = i), B = quants (column n = i): the output lanes (i, g) hold
+      // C[m = 4g + r][n = i], so every lane's four outputs belong to weight row i and need only
+      // that row's two block scales, read as an LDS broadcast (dword 0: d_even in the low half,
+      // dword 8: d_odd in the high half).
+      const f32x4 s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0, qa, zero, 0, 0, 0);
+      const f32x4 s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1, qb, zero, 0, 0, 0);
+      const float d0 = half_bits_to_float(pw[0]);
+      const float d1 = half_bits_to_float(pw[8] >> 16);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int src = 4 * g + r;
-        const float d0 = half_bits_to_float((uint32_t)__shfl((int)a0, src));
-        const float d1 = half_bits_to_float((uint32_t)__shfl((int)a2, 48 + src) >> 16);
         yacc[r] = fmaf(d0, s0[r], yacc[r]);
         yacc[r] = fmaf(d1, s1[r], yacc[r]);
       }
     }
+  };
+
+  // Rounds: wavefront w takes pairs [w P, w P + P) of each round of WAVES * P pairs. With DB the
+  // next round's loads are in flight while this round is computed (two LDS buffers, two
+  // activation register sets); the wait then leaves exactly the next round outstanding.
+  constexpr int kRoundLoads = 2 * P + kInst;
+  const int stride = WAVES * P;
+  f16x8 xa0[P], xb0[P], xa1[P], xb1[P];
+  uint32_t* buf0 = mine;
+  uint32_t* buf1 = mine + (DB ? kWaveDw : 0);
+  int p0 = wave * P;
+  if (p0 < npairs) issue(p0, buf0, xa0, xb0);
+  while (p0 < npairs) {
+    const int p1 = p0 + stride;
+    if (DB && p1 < npairs) {
+      issue(p1, buf1, xa1, xb1);
+      q8_wait_vmcnt<kRoundLoads>();
+    } else {
+      q8_wait_vmcnt<0>();
+    }
+    compute(p0, buf0, xa0, xb0);
+    if (p1 >= npairs) break;
+    if constexpr (!DB) {
+      issue(p1, buf0, xa0, xb0);
+      p0 = p1;
+      continue;
+    }
+    const int p2 = p1 + stride;
+    if (p2 < npairs) {
+      issue(p2, buf0, xa0, xb0);
+      q8_wait_vmcnt<kRoundLoads>();
+    } else {
+      q8_wait_vmcnt<0>();
+    }
+    compute(p1, buf1, xa1, xb1);
+    p0 = p2;
   }
 
   // Fold the wavefronts' partials in wavefront order (in the staging buffer, once every
@@ -169,13 +208,14 @@ __global__ void __launch_bounds__(WAVES * 64)
   for (int r = 0; r < 4; ++r) red[wave * 256 + lane * 4 + r] = yacc[r];
   __syncthreads();
   if (wave != 0) return;
+  const int n = n0 + i;  // MFMA output column = weight row
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     float s = red[lane * 4 + r];
 #pragma unroll
     for (int w = 1; w < WAVES; ++w) s += red[w * 256 + lane * 4 + r];
-    const int n = n0 + 4 * g + r;  // MFMA output row = weight row
-    if (n < N && mok) Y[(int64_t)m * N + n] = s;
+    const int mr = m0 + 4 * g + r;  // MFMA output row = activation row
+    if (n < N && mr < M) Y[(int64_t)mr * N + n] = s;
   }
 }
 
@@ -184,10 +224,10 @@ __global__ void __launch_bounds__(WAVES * 64)
 namespace uk {
 
 namespace {
-template <int WAVES, int P, int VEC>
+template <int WAVES, int P, int VEC, bool DB>
 hipError_t q8_go(const void* X, const void* Wq, float* Y, int64_t M, int64_t N, int64_t K, hipStream_t s) {
   const dim3 grid((unsigned)((N + 15) / 16), (unsigned)((M + 15) / 16));
-  hipLaunchKernelGGL((kern::q8_0_gemm_kernel<WAVES, P, VEC>), grid, dim3(WAVES * 64), 0, s,
+  hipLaunchKernelGGL((kern::q8_0_gemm_kernel<WAVES, P, VEC, DB>), grid, dim3(WAVES * 64), 0, s,
                      static_cast<const _Float16*>(X), static_cast<const uint8_t*>(Wq), Y, (int)M, (int)N, (int)K);
   return hipGetLastError();
 }
@@ -208,12 +248,15 @@ hipError_t launch_q8_gemm(const Plan& p, const void* X, const void* Wq, float* Y
   const Q8Variant v = kQ8Variants[p.variant];
   // 16-byte copies: every wavefront segment (64 P elements of K) starts 16-byte aligned.
   if (v.vec == 4 && ((K % (64 * v.pairs)) != 0 || (((uintptr_t)Wq) & 15))) return hipErrorInvalidValue;
-#define UK_Q8_CASE(W, PV, VV) \
-  if (v.waves == W && v.pairs == PV && v.vec == VV) return q8_go<W, PV, VV>(X, Wq, Y, M, N, K, s);
-  UK_Q8_CASE(16, 4, 4)
-  UK_Q8_CASE(16, 4, 1)
-  UK_Q8_CASE(8, 8, 4)
-  UK_Q8_CASE(8, 4, 1)
+#define UK_Q8_CASE(W, PV, VV, DBV) \
+  if (v.waves == W && v.pairs == PV && v.vec == VV && v.db == DBV) return q8_go<W, PV, VV, DBV != 0>(X, Wq, Y, M, N, K, s);
+  UK_Q8_CASE(16, 4, 4, 0)
+  UK_Q8_CASE(16, 4, 1, 0)
+  UK_Q8_CASE(8, 8, 4, 0)
+  UK_Q8_CASE(8, 4, 1, 0)
+  UK_Q8_CASE(8, 4, 4, 1)
+  UK_Q8_CASE(4, 4, 4, 1)
+  UK_Q8_CASE(4, 8, 4, 1)
 #undef UK_Q8_CASE
   return hipErrorInvalidValue;
 }

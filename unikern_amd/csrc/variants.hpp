@@ -53,11 +53,13 @@ constexpr int kGemmGenericTile = 64;
 // Q8_0 skinny GEMM: a workgroup owns 16 weight rows; each of its wavefronts copies `pairs`
 // block pairs of those rows per round into its own LDS area (pairs * 1088 bytes) and computes
 // them; a round covers waves * pairs block pairs. vec: dwords per lane per copy instruction
-// (4 needs K divisible by 64 * pairs).
+// (4 needs K divisible by 64 * pairs). db: two LDS buffers per wavefront, the next round's copies
+// in flight while the current round is computed.
 struct Q8Variant {
-  int waves, pairs, vec;
+  int waves, pairs, vec, db;
 };
-constexpr Q8Variant kQ8Variants[] = {{16, 4, 4}, {16, 4, 1}, {8, 8, 4}, {8, 4, 1}};
+constexpr Q8Variant kQ8Variants[] = {{16, 4, 4, 0}, {16, 4, 1, 0}, {8, 8, 4, 0}, {8, 4, 1, 0},
+                                     {8, 4, 4, 1},  {4, 4, 4, 1},  {4, 8, 4, 1}};
 constexpr int kNumQ8Variants = sizeof(kQ8Variants) / sizeof(kQ8Variants[0]);
 
 // Implicit-GEMM conv on f32 MFMA (v_mfma_f32_32x32x2f32): a wavefront owns 32 output pixels x
