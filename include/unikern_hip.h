@@ -154,6 +154,52 @@ int uk_f16_to_f32(const uint16_t* in, float* out, size_t n);
 /* Pack N rows x K int8 quants and N x K/32 binary16 scales into Q8_0 blocks (34 B each). */
 int uk_q8_0_pack(const int8_t* q, const uint16_t* d, uint8_t* blocks, int32_t N, int32_t K);
 
+/* ---- solution ledger (reference ILedger, include/unikern/components.hpp:83-125; stores
+ * src/runtime.cpp:29-176 and src/sqlite_ledger.cpp) ----
+ * A path ending in ".jsonl" opens the TAB-separated text ledger, any other path an SQLite
+ * database with the reference's schema (src/main.cpp:35-37). Keys are
+ * "op_signature|hcs_fingerprint|tree_hash" of a KML text (children included) and an HCS
+ * (NULL: the built-in MI355X description). One handle per thread. */
+int uk_ledger_open(const char* path, void** ledger);
+int uk_ledger_close(void* ledger);
+int uk_ledger_key(const char* hcs_json, const char* kml_json, char* out, size_t cap); /* length, or -1 */
+/* *hit = 1 and the recorded plan (family, variant, key, tiles; predicted_us = c_ms * 1e3) on a hit. */
+int uk_ledger_lookup(void* ledger, const char* hcs_json, const char* kml_json, uk_plan* plan, double* c_ms,
+                     double* measured_ms, double* kernel_ms, int32_t* hit);
+/* Commit a plan with its measurement (measured_ms = 0 for a solve-only row); all-or-nothing. */
+int uk_ledger_commit(void* ledger, const char* hcs_json, const char* kml_json, const uk_plan* plan,
+                     double measured_ms, double kernel_ms);
+int uk_ledger_record_violation(void* ledger, const char* hcs_json, const char* kml_json, double rate,
+                               double threshold, int32_t migrations, int32_t checks, uint64_t vram_free);
+int uk_ledger_size(void* ledger, int32_t* solutions, int32_t* violations);
+/* Measured rows of one HCS fingerprint, for calibration: up to cap rows of
+ * (c_ms, measured_ms, kernel_ms); the count is returned. */
+int uk_ledger_measured(void* ledger, const char* hcs_fp, double* rows3, int32_t cap);
+/* Calibration closure (reference src/solver.cpp:194-244, src/main.cpp:579-652): the HCS with
+ * link_bw_gbps replaced by the median host-link rate of this HCS's measured ledger rows
+ * ((bytes) / (measured_ms - kernel_ms)) and constants_version + 1. 3 when no row is usable. */
+int uk_calibrate(const char* hcs_json, void* ledger, char* out_json, size_t cap, char* detail, size_t detail_cap);
+/* The HCS with its device tier set to `bytes` (re-solve on a measured capacity,
+ * reference src/main.cpp:488-515). */
+int uk_hcs_with_capacity(const char* hcs_json, uint64_t bytes, char* out_json, size_t cap);
+
+/* ---- GGUF weights (format as read by the reference's probe/phase63_gguf_header.py; no
+ * counterpart on the reference's execution path, which has no Q8_0 kernel) ----
+ * Reads the header, metadata and tensor directory; Q8_0 tensors [ne0 = K, ne1 = N] are the
+ * Q8_0 GEMM's weight layout byte for byte. ggml types: 0 f32, 1 f16, 8 q8_0, 30 bf16. */
+int uk_gguf_open(const char* path, void** file);
+int uk_gguf_close(void* file);
+int32_t uk_gguf_tensor_count(void* file);
+int32_t uk_gguf_find(void* file, const char* name); /* index, or -1 */
+int uk_gguf_tensor_info(void* file, int32_t index, char* name, size_t cap, int32_t* ggml_type, int32_t* n_dims,
+                        int64_t* ne4, uint64_t* file_offset, uint64_t* nbytes);
+int uk_gguf_metadata(void* file, const char* key, char* out, size_t cap); /* length, or -1 */
+int uk_gguf_read(void* file, int32_t index, void* host_dst, uint64_t cap);
+/* Copy a tensor's bytes into device memory (host staging, then one copy). */
+int uk_gguf_upload(void* file, int32_t index, void* dev_dst, uint64_t cap);
+/* The Q8_0 GEMM of M activation rows against a 2-D Q8_0 tensor: gemm q8_0 TN [M, ne1, ne0]. */
+int uk_gguf_q8_0_desc(void* file, int32_t index, int32_t M, uk_op_desc* out);
+
 /* ---- device memory, streams and events (plumbing for callers without a runtime) ---- */
 int uk_malloc(void** p, size_t bytes);
 int uk_free(void* p);

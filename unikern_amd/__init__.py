@@ -25,6 +25,7 @@ from ._capi import (DTYPES, FAMILIES, LAYOUTS, OPS, UK_BAD_INVOCATION, UK_HIP_FA
                     UK_RESIDENCY, UK_VERIFY_FAIL, OpDesc, Plan, Result)
 
 lib = _capi.load()
+CLI = Path(__file__).resolve().parent / "unikern"  # the command-line front door (built with the library)
 
 SEED = 20261201
 ROOT = Path(__file__).resolve().parent.parent
@@ -285,3 +286,177 @@ def launch(d: OpDesc, ins, out: DeviceBuffer, plan: Plan | None = None, stream=N
 
 def synchronize():
     _check(lib.uk_synchronize())
+
+
+# ---------------------------------------------------------------------------------------
+# Solution ledger (reference ILedger: include/unikern/components.hpp:83-125)
+# ---------------------------------------------------------------------------------------
+@dataclass
+class LedgerHit:
+    plan: Plan
+    c_ms: float
+    measured_ms: float
+    kernel_ms: float
+
+
+class Ledger:
+    """A ".jsonl" path opens the text ledger, any other path SQLite (the reference's schema)."""
+
+    def __init__(self, path: str | Path):
+        h = C.c_void_p()
+        _check(lib.uk_ledger_open(str(path).encode(), C.byref(h)))
+        self._h = h
+
+    def close(self):
+        if self._h:
+            lib.uk_ledger_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @staticmethod
+    def key(kml_text: str, hcs_json: str | None = None) -> str:
+        out = _buf(4096)
+        if lib.uk_ledger_key(None if hcs_json is None else _text(hcs_json), _text(kml_text), out, len(out)) < 0:
+            raise UnikernError(UK_BAD_INVOCATION, last_error())
+        return out.value.decode()
+
+    def lookup(self, kml_text: str, hcs_json: str | None = None) -> LedgerHit | None:
+        p, c, m, k, hit = Plan(), C.c_double(), C.c_double(), C.c_double(), C.c_int32()
+        _check(lib.uk_ledger_lookup(self._h, None if hcs_json is None else _text(hcs_json), _text(kml_text),
+                                    C.byref(p), C.byref(c), C.byref(m), C.byref(k), C.byref(hit)))
+        return LedgerHit(p, c.value, m.value, k.value) if hit.value else None
+
+    def commit(self, kml_text: str, plan: Plan, measured_ms: float = 0.0, kernel_ms: float = 0.0,
+               hcs_json: str | None = None):
+        _check(lib.uk_ledger_commit(self._h, None if hcs_json is None else _text(hcs_json), _text(kml_text),
+                                    C.byref(plan), measured_ms, kernel_ms))
+
+    def record_violation(self, kml_text: str, rate: float, threshold: float, migrations: int, checks: int,
+                         vram_free: int, hcs_json: str | None = None):
+        _check(lib.uk_ledger_record_violation(self._h, None if hcs_json is None else _text(hcs_json),
+                                              _text(kml_text), rate, threshold, migrations, checks, vram_free))
+
+    def size(self) -> tuple[int, int]:
+        s, v = C.c_int32(), C.c_int32()
+        _check(lib.uk_ledger_size(self._h, C.byref(s), C.byref(v)))
+        return s.value, v.value
+
+    def measured(self, hcs_fp: str) -> list[tuple[float, float, float]]:
+        n = lib.uk_ledger_measured(self._h, hcs_fp.encode(), None, 0)
+        if n < 0:
+            raise UnikernError(UK_BAD_INVOCATION, last_error())
+        rows = (C.c_double * (3 * max(n, 1)))()
+        lib.uk_ledger_measured(self._h, hcs_fp.encode(), rows, n)
+        return [(rows[3 * i], rows[3 * i + 1], rows[3 * i + 2]) for i in range(n)]
+
+    def calibrate(self, hcs_json: str | None = None) -> tuple[str, str]:
+        """(calibrated HCS text, detail) — link_bw_gbps from this ledger's measured rows."""
+        out, detail = _buf(1 << 16), _buf(1 << 16)
+        rc = lib.uk_calibrate(None if hcs_json is None else _text(hcs_json), self._h, out, len(out), detail,
+                              len(detail))
+        if rc != UK_OK:
+            raise UnikernError(rc, detail.value.decode())
+        return out.value.decode(), detail.value.decode()
+
+
+def hcs_with_capacity(hcs_json: str | None, nbytes: int) -> str:
+    out = _buf(1 << 16)
+    _check(lib.uk_hcs_with_capacity(None if hcs_json is None else _text(hcs_json), nbytes, out, len(out)))
+    return out.value.decode()
+
+
+# ---------------------------------------------------------------------------------------
+# GGUF weights
+# ---------------------------------------------------------------------------------------
+GGML_TYPES = {0: "f32", 1: "f16", 8: "q8_0", 30: "bf16"}
+
+
+@dataclass
+class GgufTensor:
+    index: int
+    name: str
+    ggml_type: int
+    ne: tuple
+    offset: int
+    nbytes: int
+
+    @property
+    def type_name(self) -> str:
+        return GGML_TYPES.get(self.ggml_type, f"type{self.ggml_type}")
+
+
+class Gguf:
+    """Header, metadata and tensor directory of a GGUF file; tensor bytes to host or device."""
+
+    def __init__(self, path: str | Path):
+        h = C.c_void_p()
+        _check(lib.uk_gguf_open(str(path).encode(), C.byref(h)))
+        self._h = h
+
+    def close(self):
+        if self._h:
+            lib.uk_gguf_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __len__(self) -> int:
+        return lib.uk_gguf_tensor_count(self._h)
+
+    def tensor(self, key: int | str) -> GgufTensor:
+        idx = key if isinstance(key, int) else lib.uk_gguf_find(self._h, key.encode())
+        if idx < 0:
+            raise KeyError(key)
+        name = _buf(4096)
+        t, nd = C.c_int32(), C.c_int32()
+        ne = (C.c_int64 * 4)()
+        off, nb = C.c_uint64(), C.c_uint64()
+        _check(lib.uk_gguf_tensor_info(self._h, idx, name, len(name), C.byref(t), C.byref(nd), ne, C.byref(off),
+                                       C.byref(nb)))
+        return GgufTensor(idx, name.value.decode(), t.value, tuple(ne[: nd.value]), off.value, nb.value)
+
+    def tensors(self) -> list[GgufTensor]:
+        return [self.tensor(i) for i in range(len(self))]
+
+    def metadata(self, key: str) -> str | None:
+        out = _buf(1 << 16)
+        n = lib.uk_gguf_metadata(self._h, key.encode(), out, len(out))
+        return None if n < 0 else out.value.decode()
+
+    def read(self, key: int | str) -> np.ndarray:
+        t = self.tensor(key)
+        out = np.empty(t.nbytes, np.uint8)
+        _check(lib.uk_gguf_read(self._h, t.index, out.ctypes.data_as(C.c_void_p), out.nbytes))
+        return out
+
+    def upload(self, key: int | str) -> "DeviceBuffer":
+        t = self.tensor(key)
+        buf = DeviceBuffer(t.nbytes)
+        _check(lib.uk_gguf_upload(self._h, t.index, buf.ptr, t.nbytes))
+        return buf
+
+    def q8_0_desc(self, key: int | str, M: int) -> OpDesc:
+        d = OpDesc()
+        _check(lib.uk_gguf_q8_0_desc(self._h, self.tensor(key).index, M, C.byref(d)))
+        return d

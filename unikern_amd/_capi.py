@@ -69,6 +69,28 @@ _SIG = {
     "uk_f32_to_f16": ([_P, _P, C.c_size_t], C.c_int),
     "uk_f16_to_f32": ([_P, _P, C.c_size_t], C.c_int),
     "uk_q8_0_pack": ([_P, _P, _P, C.c_int32, C.c_int32], C.c_int),
+    "uk_ledger_open": ([C.c_char_p, C.POINTER(_P)], C.c_int),
+    "uk_ledger_close": ([_P], C.c_int),
+    "uk_ledger_key": ([C.c_char_p, C.c_char_p, C.c_char_p, C.c_size_t], C.c_int),
+    "uk_ledger_lookup": ([_P, C.c_char_p, C.c_char_p, C.POINTER(Plan), C.POINTER(C.c_double), C.POINTER(C.c_double),
+                          C.POINTER(C.c_double), C.POINTER(C.c_int32)], C.c_int),
+    "uk_ledger_commit": ([_P, C.c_char_p, C.c_char_p, C.POINTER(Plan), C.c_double, C.c_double], C.c_int),
+    "uk_ledger_record_violation": ([_P, C.c_char_p, C.c_char_p, C.c_double, C.c_double, C.c_int32, C.c_int32,
+                                    C.c_uint64], C.c_int),
+    "uk_ledger_size": ([_P, C.POINTER(C.c_int32), C.POINTER(C.c_int32)], C.c_int),
+    "uk_ledger_measured": ([_P, C.c_char_p, C.POINTER(C.c_double), C.c_int32], C.c_int),
+    "uk_calibrate": ([C.c_char_p, _P, C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t], C.c_int),
+    "uk_hcs_with_capacity": ([C.c_char_p, C.c_uint64, C.c_char_p, C.c_size_t], C.c_int),
+    "uk_gguf_open": ([C.c_char_p, C.POINTER(_P)], C.c_int),
+    "uk_gguf_close": ([_P], C.c_int),
+    "uk_gguf_tensor_count": ([_P], C.c_int32),
+    "uk_gguf_find": ([_P, C.c_char_p], C.c_int32),
+    "uk_gguf_tensor_info": ([_P, C.c_int32, C.c_char_p, C.c_size_t, C.POINTER(C.c_int32), C.POINTER(C.c_int32),
+                             C.POINTER(C.c_int64), C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)], C.c_int),
+    "uk_gguf_metadata": ([_P, C.c_char_p, C.c_char_p, C.c_size_t], C.c_int),
+    "uk_gguf_read": ([_P, C.c_int32, _P, C.c_uint64], C.c_int),
+    "uk_gguf_upload": ([_P, C.c_int32, _P, C.c_uint64], C.c_int),
+    "uk_gguf_q8_0_desc": ([_P, C.c_int32, C.c_int32, C.POINTER(OpDesc)], C.c_int),
     "uk_malloc": ([C.POINTER(_P), C.c_size_t], C.c_int),
     "uk_free": ([_P], C.c_int),
     "uk_memcpy_htod": ([_P, _P, C.c_size_t], C.c_int),

@@ -19,6 +19,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
 LIB = PKG / "libunikern_hip.so"
+CLI = PKG / "unikern"
 ROOT = PKG.parent
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -63,13 +64,21 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(_compile, srcs))
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs), "-lpthread"]
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs), "-lpthread", "-ldl"]
     p = subprocess.run(cmd, capture_output=True, text=True)
     if p.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{p.stdout}\n{p.stderr}")
     os.replace(tmp, LIB)
+    # The command-line front door, over the C ABI only; finds the library next to itself.
+    cli_tmp = CLI.with_suffix(".tmp")
+    cmd = [CXX, "-O2", "-std=c++20", "-Wall", f"-I{ROOT / 'include'}", str(CSRC / "cli" / "unikern.cpp"), "-o",
+           str(cli_tmp), f"-L{PKG}", "-lunikern_hip", "-Wl,-rpath,$ORIGIN", "-Wl,-rpath-link,/opt/rocm/lib"]
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    if p.returncode != 0:
+        raise RuntimeError(f"CLI build failed: {' '.join(cmd)}\n{p.stdout}\n{p.stderr}")
+    os.replace(cli_tmp, CLI)
     if verbose:
-        print(f"built {LIB} from {len(objs)} objects")
+        print(f"built {LIB} from {len(objs)} objects, and {CLI}")
     return LIB
 
 

@@ -19,7 +19,10 @@
 #include <vector>
 
 #include "../../include/unikern_hip.h"
+#include "host/calibrate.hpp"
+#include "host/gguf.hpp"
 #include "host/inputs.hpp"
+#include "host/ledger.hpp"
 #include "host/uk_core.hpp"
 #include "launch.hpp"
 #include "variants.hpp"
@@ -1041,6 +1044,240 @@ int uk_event_record(void* ev, void* s) {
 }
 int uk_event_elapsed_ms(void* a, void* b, float* ms) {
   return hip_rc(hipEventElapsedTime(ms, static_cast<hipEvent_t>(a), static_cast<hipEvent_t>(b)), "hipEventElapsedTime");
+}
+
+// ---- solution ledger ----
+namespace {
+bool ledger_key_of(const char* hcs_json, const char* kml_json, LedgerKey* key, KmlTree* tree) {
+  Hcs h;
+  std::string e;
+  if (!load_hcs(hcs_json, &h, &e)) return fail(UK_BAD_INVOCATION, e), false;
+  if (!kml_json) return fail(UK_BAD_INVOCATION, "null KML"), false;
+  auto t = kml_import(kml_json, &e);
+  if (!t) return fail(UK_BAD_INVOCATION, e), false;
+  key->op_sig = op_signature(*t);
+  key->hcs_fp = hcs_fingerprint(h);
+  key->tree_hash = fnv1a_hex(canonical_form(*t));
+  if (tree) *tree = *t;
+  return true;
+}
+Ledger* as_ledger(void* p) { return static_cast<Ledger*>(p); }
+GgufFile* as_gguf(void* p) { return static_cast<GgufFile*>(p); }
+}  // namespace
+
+int uk_ledger_open(const char* path, void** ledger) {
+  if (!path || !ledger) return fail(UK_BAD_INVOCATION, "null argument");
+  std::string e;
+  auto l = open_ledger(path, &e);
+  if (!l) return fail(UK_BAD_INVOCATION, e);
+  *ledger = l.release();
+  return UK_OK;
+}
+
+int uk_ledger_close(void* ledger) {
+  delete as_ledger(ledger);
+  return UK_OK;
+}
+
+int uk_ledger_key(const char* hcs_json, const char* kml_json, char* out, size_t cap) {
+  LedgerKey k;
+  if (!ledger_key_of(hcs_json, kml_json, &k, nullptr)) return -1;
+  return put(k.composite(), out, cap);
+}
+
+int uk_ledger_lookup(void* ledger, const char* hcs_json, const char* kml_json, uk_plan* plan, double* c_ms,
+                     double* measured_ms, double* kernel_ms, int32_t* hit) {
+  if (!ledger || !hit) return fail(UK_BAD_INVOCATION, "null argument");
+  *hit = 0;
+  LedgerKey k;
+  if (!ledger_key_of(hcs_json, kml_json, &k, nullptr)) return UK_BAD_INVOCATION;
+  auto row = as_ledger(ledger)->lookup(k);
+  if (!row) return UK_OK;
+  std::string key;
+  int fam = 0, var = 0;
+  if (!parse_placement(row->placement, &key, &fam, &var))
+    return fail(UK_BAD_INVOCATION, "ledger row of " + k.composite() + " records no plan: " + row->placement);
+  if (plan) {
+    std::memset(plan, 0, sizeof *plan);
+    plan->family = fam;
+    plan->variant = var;
+    plan->tile_m = row->tile_m;
+    plan->tile_n = row->tile_n;
+    plan->predicted_us = row->c_ms * 1e3;
+    plan->feasible = 1;
+    std::snprintf(plan->key, sizeof plan->key, "%s", key.c_str());
+  }
+  if (c_ms) *c_ms = row->c_ms;
+  if (measured_ms) *measured_ms = row->measured_ms;
+  if (kernel_ms) *kernel_ms = row->kernel_ms;
+  *hit = 1;
+  return UK_OK;
+}
+
+int uk_ledger_commit(void* ledger, const char* hcs_json, const char* kml_json, const uk_plan* plan,
+                     double measured_ms, double kernel_ms) {
+  if (!ledger || !plan) return fail(UK_BAD_INVOCATION, "null argument");
+  LedgerKey k;
+  if (!ledger_key_of(hcs_json, kml_json, &k, nullptr)) return UK_BAD_INVOCATION;
+  LedgerRow r;
+  r.c_ms = plan->predicted_us * 1e-3;
+  r.measured_ms = measured_ms;
+  r.kernel_ms = kernel_ms;
+  r.tile_m = plan->tile_m;
+  r.tile_n = plan->tile_n;
+  r.placement = placement_of(std::string(plan->key, strnlen(plan->key, sizeof plan->key)), plan->family,
+                             plan->variant, "grid=" + std::to_string(plan->grid) + " threads=" +
+                                                std::to_string(plan->threads));
+  std::string e;
+  if (!as_ledger(ledger)->commit(k, r, &e)) return fail(UK_HIP_FAILURE, e);
+  return UK_OK;
+}
+
+int uk_ledger_record_violation(void* ledger, const char* hcs_json, const char* kml_json, double rate,
+                               double threshold, int32_t migrations, int32_t checks, uint64_t vram_free) {
+  if (!ledger) return fail(UK_BAD_INVOCATION, "null argument");
+  LedgerKey k;
+  if (!ledger_key_of(hcs_json, kml_json, &k, nullptr)) return UK_BAD_INVOCATION;
+  std::string e;
+  if (!as_ledger(ledger)->record_violation(k, rate, threshold, migrations, checks, vram_free, &e))
+    return fail(UK_HIP_FAILURE, e);
+  return UK_OK;
+}
+
+int uk_ledger_size(void* ledger, int32_t* solutions, int32_t* violations) {
+  if (!ledger) return fail(UK_BAD_INVOCATION, "null argument");
+  if (solutions) *solutions = as_ledger(ledger)->size();
+  if (violations) *violations = as_ledger(ledger)->violation_count();
+  return UK_OK;
+}
+
+int uk_ledger_measured(void* ledger, const char* hcs_fp, double* rows3, int32_t cap) {
+  if (!ledger || !hcs_fp) return fail(UK_BAD_INVOCATION, "null argument"), -1;
+  const auto rows = as_ledger(ledger)->measured_rows(hcs_fp);
+  for (int32_t i = 0; i < cap && i < (int32_t)rows.size(); ++i) {
+    rows3[3 * i] = rows[i].c_ms;
+    rows3[3 * i + 1] = rows[i].measured_ms;
+    rows3[3 * i + 2] = rows[i].kernel_ms;
+  }
+  return (int)rows.size();
+}
+
+int uk_calibrate(const char* hcs_json, void* ledger, char* out_json, size_t cap, char* detail, size_t detail_cap) {
+  if (!ledger) return fail(UK_BAD_INVOCATION, "null ledger");
+  Hcs h;
+  std::string e;
+  if (!load_hcs(hcs_json, &h, &e)) return fail(UK_BAD_INVOCATION, e);
+  const auto rows = as_ledger(ledger)->measured_rows(hcs_fingerprint(h));
+  if (rows.empty()) {
+    put("no measured rows for hcs_fp=" + hcs_fingerprint(h).substr(0, 8) + " (run first, then calibrate)", detail,
+        detail_cap);
+    return fail(UK_INFEASIBLE, "no measured rows");
+  }
+  std::string d;
+  const double bw = calibrated_link_bw(rows, &d);
+  put(d, detail, detail_cap);
+  if (bw <= 0) return fail(UK_INFEASIBLE, d);
+  h.link_bw_gbps = bw;
+  h.constants_version += 1;
+  put(hcs_export(h), out_json, cap);
+  return UK_OK;
+}
+
+int uk_hcs_with_capacity(const char* hcs_json, uint64_t bytes, char* out_json, size_t cap) {
+  Hcs h;
+  std::string e;
+  if (!load_hcs(hcs_json, &h, &e)) return fail(UK_BAD_INVOCATION, e);
+  bool applied = false;
+  for (auto& t : h.tiers)
+    if (t.name == "vram" || t.name == "unified") {
+      t.bytes = (int64_t)bytes;
+      t.confidence = Confidence::Measured;
+      applied = true;
+    }
+  if (!applied) return fail(UK_BAD_INVOCATION, "the HCS declares no device tier");
+  put(hcs_export(h), out_json, cap);
+  return UK_OK;
+}
+
+// ---- GGUF weights ----
+int uk_gguf_open(const char* path, void** file) {
+  if (!path || !file) return fail(UK_BAD_INVOCATION, "null argument");
+  std::string e;
+  auto g = gguf_open(path, &e);
+  if (!g) return fail(UK_BAD_INVOCATION, e);
+  *file = new GgufFile(std::move(*g));
+  return UK_OK;
+}
+
+int uk_gguf_close(void* file) {
+  delete as_gguf(file);
+  return UK_OK;
+}
+
+int32_t uk_gguf_tensor_count(void* file) { return file ? (int32_t)as_gguf(file)->tensors.size() : -1; }
+
+int32_t uk_gguf_find(void* file, const char* name) {
+  return (file && name) ? gguf_find(*as_gguf(file), name) : -1;
+}
+
+int uk_gguf_tensor_info(void* file, int32_t index, char* name, size_t cap, int32_t* ggml_type, int32_t* n_dims,
+                        int64_t* ne4, uint64_t* file_offset, uint64_t* nbytes) {
+  if (!file) return fail(UK_BAD_INVOCATION, "null argument");
+  const GgufFile& g = *as_gguf(file);
+  if (index < 0 || index >= (int32_t)g.tensors.size()) return fail(UK_BAD_INVOCATION, "tensor index out of range");
+  const GgufTensor& t = g.tensors[index];
+  put(t.name, name, cap);
+  if (ggml_type) *ggml_type = (int32_t)t.type;
+  if (n_dims) *n_dims = (int32_t)t.ne.size();
+  if (ne4)
+    for (int i = 0; i < 4; ++i) ne4[i] = i < (int)t.ne.size() ? t.ne[i] : 1;
+  if (file_offset) *file_offset = t.offset;
+  if (nbytes) *nbytes = t.nbytes;
+  return UK_OK;
+}
+
+int uk_gguf_metadata(void* file, const char* key, char* out, size_t cap) {
+  if (!file || !key) return -1;
+  const auto& kv = as_gguf(file)->kv;
+  const auto it = kv.find(key);
+  return it == kv.end() ? -1 : put(it->second, out, cap);
+}
+
+int uk_gguf_read(void* file, int32_t index, void* host_dst, uint64_t cap) {
+  if (!file || !host_dst) return fail(UK_BAD_INVOCATION, "null argument");
+  std::string e;
+  if (!gguf_read(*as_gguf(file), index, host_dst, cap, &e)) return fail(UK_BAD_INVOCATION, e);
+  return UK_OK;
+}
+
+int uk_gguf_upload(void* file, int32_t index, void* dev_dst, uint64_t cap) {
+  if (!file || !dev_dst) return fail(UK_BAD_INVOCATION, "null argument");
+  const GgufFile& g = *as_gguf(file);
+  if (index < 0 || index >= (int32_t)g.tensors.size()) return fail(UK_BAD_INVOCATION, "tensor index out of range");
+  std::vector<uint8_t> host(g.tensors[index].nbytes);
+  std::string e;
+  if (!gguf_read(g, index, host.data(), std::min<uint64_t>(cap, host.size()), &e)) return fail(UK_BAD_INVOCATION, e);
+  return hip_rc(hipMemcpy(dev_dst, host.data(), host.size(), hipMemcpyHostToDevice), "hipMemcpy gguf tensor");
+}
+
+int uk_gguf_q8_0_desc(void* file, int32_t index, int32_t M, uk_op_desc* out) {
+  if (!file || !out || M <= 0) return fail(UK_BAD_INVOCATION, "bad argument");
+  const GgufFile& g = *as_gguf(file);
+  if (index < 0 || index >= (int32_t)g.tensors.size()) return fail(UK_BAD_INVOCATION, "tensor index out of range");
+  const GgufTensor& t = g.tensors[index];
+  if (t.type != kGgmlQ8_0) return fail(UK_BAD_INVOCATION, "tensor '" + t.name + "' is " + ggml_type_name(t.type) + ", not q8_0");
+  if (t.ne.size() != 2) return fail(UK_BAD_INVOCATION, "tensor '" + t.name + "' is not 2-D");
+  if (t.ne[0] > INT32_MAX || t.ne[1] > INT32_MAX) return fail(UK_BAD_INVOCATION, "tensor too large for a KML dim");
+  KmlTree tr;
+  tr.op = OpKind::Gemm;
+  tr.dtype = DType::Q8_0;
+  tr.layout = Layout::TN;
+  tr.ndims = 3;
+  tr.dims[0] = M;
+  tr.dims[1] = (int)t.ne[1];
+  tr.dims[2] = (int)t.ne[0];
+  desc_of(tr, out);
+  return UK_OK;
 }
 
 }  // extern "C"

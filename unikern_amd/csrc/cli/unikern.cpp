@@ -1,0 +1,497 @@
+// unikern — the command-line front door of the MI355X path, over the C ABI only
+// (include/unikern_hip.h), as the reference's CLI is over its library (src/main.cpp:276-736).
+//
+//   unikern kml <file.json>
+//   unikern hcs <file.json | builtin>
+//   unikern solve --hcs f [--ledger l] [--kml f.json | --op OP --dims D...] [--selfcheck]
+//   unikern run    --hcs f [--ledger l] [--kml f.json | --op OP --dims D...] [--iters n] [--seed s]
+//                  [--exact] [--migration-threshold r]
+//   unikern verify (as run; never writes the ledger)
+//   unikern calibrate --hcs f --ledger l [--out f.json]
+//   unikern backends
+//
+// Output lines and exit codes follow the reference: COVER, SOLVED / LEDGER HIT, RUN, the
+// UNIKERN_RESULT line in the log tail, UNIKERN_VIOLATION, RESOLVE, LEDGER COMMIT, VERIFY PASS;
+// 0 pass, 1 verify failure, 2 bad invocation or unsupported tree, 3 infeasible, 5 residency.
+// "--hcs builtin" names the library's MI355X description. A ledger path ending in .jsonl is the
+// text ledger, any other path SQLite (default ledger.sqlite3, as in the reference).
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <iostream>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "unikern_hip.h"
+
+namespace {
+
+struct Options {
+  std::string hcs_path, kml_path, ledger = "ledger.sqlite3", out_path, op = "gemm";
+  std::vector<long> dims;
+  std::string dtype = "fp32";
+  bool selfcheck = false, exact = false;
+  int iters = 50;
+  unsigned long long seed = 20261201ULL;
+  double migration_threshold = 0.0;
+};
+
+std::string last_error() {
+  const char* e = uk_last_error();
+  return e ? e : "";
+}
+
+bool read_file(const std::string& path, std::string* out) {
+  std::ifstream in(path, std::ios::binary);
+  if (!in) return false;
+  std::stringstream ss;
+  ss << in.rdbuf();
+  *out = ss.str();
+  return true;
+}
+
+bool parse(int argc, char** argv, Options* o) {
+  for (int i = 0; i < argc; ++i) {
+    const std::string a = argv[i];
+    auto next = [&](std::string* v) {
+      if (i + 1 >= argc) return false;
+      *v = argv[++i];
+      return true;
+    };
+    std::string v;
+    if (a == "--hcs") { if (!next(&o->hcs_path)) return false; }
+    else if (a == "--kml") { if (!next(&o->kml_path)) return false; }
+    else if (a == "--ledger") { if (!next(&o->ledger)) return false; }
+    else if (a == "--out") { if (!next(&o->out_path)) return false; }
+    else if (a == "--op") { if (!next(&o->op)) return false; }
+    else if (a == "--dtype") { if (!next(&o->dtype)) return false; }
+    else if (a == "--dims") {
+      while (i + 1 < argc && argv[i + 1][0] != '-') o->dims.push_back(std::strtol(argv[++i], nullptr, 10));
+    } else if (a == "--iters") { if (!next(&v)) return false; o->iters = std::atoi(v.c_str()); }
+    else if (a == "--seed") { if (!next(&v)) return false; o->seed = std::strtoull(v.c_str(), nullptr, 10); }
+    else if (a == "--migration-threshold") { if (!next(&v)) return false; o->migration_threshold = std::atof(v.c_str()); }
+    else if (a == "--selfcheck") o->selfcheck = true;
+    else if (a == "--exact") o->exact = true;
+    else {
+      std::cerr << "unknown argument: " << a << "\n";
+      return false;
+    }
+  }
+  return true;
+}
+
+// The HCS text (empty = built-in) or false when the file cannot be read or is rejected.
+bool load_hcs(const Options& o, std::string* text) {
+  if (o.hcs_path == "builtin") {
+    text->clear();
+    return true;
+  }
+  if (!read_file(o.hcs_path, text)) {
+    std::cerr << "cannot read HCS file: " << o.hcs_path << "\n";
+    return false;
+  }
+  char buf[4096];
+  if (uk_hcs_fingerprint(text->c_str(), buf, sizeof buf) != UK_OK) {
+    std::cerr << "HCS rejected: " << buf << "\n";
+    return false;
+  }
+  return true;
+}
+const char* hcs_arg(const std::string& text) { return text.empty() ? nullptr : text.c_str(); }
+
+// The declared workload as KML text: the --kml file, or the --op/--dims shorthand.
+bool load_kml(const Options& o, std::string* text) {
+  if (!o.kml_path.empty()) {
+    if (!read_file(o.kml_path, text)) {
+      std::cerr << "cannot read KML file: " << o.kml_path << "\n";
+      return false;
+    }
+  } else {
+    std::ostringstream os;
+    os << "{\"op\": \"" << o.op << "\", \"dtype\": \"" << o.dtype << "\", \"dims\": [";
+    std::vector<long> d = o.dims;
+    if (d.empty()) d = o.op == "gemm" ? std::vector<long>{4096, 4096, 4096} : std::vector<long>{1048576};
+    for (size_t i = 0; i < d.size(); ++i) os << (i ? ", " : "") << d[i];
+    os << "]}";
+    *text = os.str();
+  }
+  uk_op_desc d;
+  char err[8192];
+  if (uk_kml_import(text->c_str(), &d, err, sizeof err) != UK_OK) {
+    std::cerr << "KML " << err << "\n";
+    return false;
+  }
+  return true;
+}
+
+std::string gap_of(const std::string& kml) {
+  uk_op_desc d;
+  char err[4096];
+  uk_kml_import(kml.c_str(), &d, err, sizeof err);
+  char reason[4096] = {0};
+  return uk_support_gap(&d, reason, sizeof reason) == UK_OK ? "" : reason;
+}
+
+void print_coverage(const std::string& gap) {
+  std::cout << "COVER amd:hip primitive=" << (gap.empty() ? "covered" : "unsupported");
+  if (!gap.empty()) std::cout << " reason=" << gap;
+  std::cout << " execution=resident-only toolchain=present\n";
+}
+
+std::string fp8(const std::string& hcs) {
+  char fp[64];
+  uk_hcs_fingerprint(hcs_arg(hcs), fp, sizeof fp);
+  return std::string(fp).substr(0, 8);
+}
+
+struct Solved {
+  uk_plan plan{};
+  std::string log;
+  int rc = 0;
+};
+
+Solved solve_tree(const std::string& hcs, const std::string& kml) {
+  Solved s;
+  uk_op_desc d;
+  char err[4096];
+  uk_kml_import(kml.c_str(), &d, err, sizeof err);
+  std::vector<char> log(1 << 16);
+  s.rc = uk_solve(hcs_arg(hcs), &d, &s.plan, log.data(), log.size());
+  s.log = log.data();
+  return s;
+}
+
+void* open_ledger(const std::string& path) {
+  void* l = nullptr;
+  if (uk_ledger_open(path.c_str(), &l) != UK_OK) {
+    std::cerr << "ledger: " << last_error() << "\n";
+    return nullptr;
+  }
+  return l;
+}
+
+int cmd_kml(const std::string& path) {
+  std::string text;
+  if (!read_file(path, &text)) {
+    std::cerr << "cannot read KML file: " << path << "\n";
+    return 2;
+  }
+  uk_op_desc d;
+  char err[8192];
+  if (uk_kml_import(text.c_str(), &d, err, sizeof err) != UK_OK) {
+    std::cerr << "INVALID " << err << "\n";
+    return 2;
+  }
+  char sig[512], hash[64];
+  uk_op_signature(&d, sig, sizeof sig);
+  uk_kml_tree_hash(text.c_str(), hash, sizeof hash);
+  int64_t ops = 0, bytes = 0, wbytes = 0;
+  uk_workload(&d, &ops, &bytes, &wbytes);
+  std::vector<char> canon(1 << 16);
+  uk_kml_canonical(text.c_str(), canon.data(), canon.size());
+  std::cout << "VALID  " << sig << "  tree_hash=" << hash << "  ops=" << ops << "  bytes=" << bytes;
+  if (wbytes) std::cout << "  weight_bytes=" << wbytes;
+  std::cout << "\n" << canon.data() << "\n";
+  print_coverage(gap_of(text));
+  return 0;
+}
+
+int cmd_hcs(const std::string& path) {
+  Options o;
+  o.hcs_path = path;
+  std::string text;
+  if (!load_hcs(o, &text)) return 2;
+  std::vector<char> out(1 << 16);
+  char fp[64];
+  uk_hcs_fingerprint(hcs_arg(text), fp, sizeof fp);
+  uk_hcs_export(hcs_arg(text), out.data(), out.size());
+  std::cout << "VALID  hcs_fp=" << fp << "\n" << out.data();
+  return 0;
+}
+
+int cmd_solve(int argc, char** argv) {
+  Options o;
+  if (!parse(argc, argv, &o) || o.hcs_path.empty()) {
+    std::cerr << "usage: unikern solve --hcs <file.json|builtin> [--ledger f] [--kml f.json | --op OP --dims D...] "
+                 "[--selfcheck]\n";
+    return 2;
+  }
+  std::string hcs, kml;
+  if (!load_hcs(o, &hcs) || !load_kml(o, &kml)) return 2;
+  const std::string gap = gap_of(kml);
+  if (!gap.empty()) {
+    std::cerr << "UNSUPPORTED: " << gap << " — solve files no ledger row for a tree no kernel covers.\n";
+    return 2;
+  }
+  void* ledger = open_ledger(o.ledger);
+  if (!ledger) return 2;
+  uk_plan plan;
+  double c_ms = 0, measured = 0, kernel = 0;
+  int32_t hit = 0;
+  if (uk_ledger_lookup(ledger, hcs_arg(hcs), kml.c_str(), &plan, &c_ms, &measured, &kernel, &hit) != UK_OK) {
+    std::cerr << "ledger: " << last_error() << "\n";
+    uk_ledger_close(ledger);
+    return 2;
+  }
+  if (hit) {
+    std::cout << "LEDGER HIT  c_cached_ms=" << c_ms << "  tile=" << plan.tile_m << "x" << plan.tile_n
+              << "  plan=" << plan.key << "\n";
+    print_coverage(gap);
+    uk_ledger_close(ledger);
+    return 0;
+  }
+  const Solved s = solve_tree(hcs, kml);
+  if (s.rc == UK_INFEASIBLE) {
+    std::cerr << "INFEASIBLE: " << s.log << "\n";
+    uk_ledger_close(ledger);
+    return 3;
+  }
+  if (s.rc != UK_OK) {
+    std::cerr << "solve: " << s.log << "\n";
+    uk_ledger_close(ledger);
+    return 2;
+  }
+  std::cout << "SOLVED  x* tile=" << s.plan.tile_m << "x" << s.plan.tile_n << "  c_ms=" << s.plan.predicted_us * 1e-3
+            << "  |X|=" << s.plan.feasible << "  hcs_fp=" << fp8(hcs) << "\n"
+            << s.log << "\n";
+  print_coverage(gap);
+  // solve has no measurement: the row carries the prediction, replaced by run's measurement.
+  if (uk_ledger_commit(ledger, hcs_arg(hcs), kml.c_str(), &s.plan, s.plan.predicted_us * 1e-3, 0.0) != UK_OK)
+    std::cerr << "ledger commit failed: " << last_error() << "\n";
+  uk_ledger_close(ledger);
+  if (o.selfcheck) {  // solve is a pure function of (hcs, tree)
+    const Solved again = solve_tree(hcs, kml);
+    const bool ok = again.rc == UK_OK && again.plan.predicted_us == s.plan.predicted_us &&
+                    std::strcmp(again.plan.key, s.plan.key) == 0;
+    std::cout << (ok ? "SELFCHECK OK (deterministic)" : "SELFCHECK FAIL") << "\n";
+    return ok ? 0 : 1;
+  }
+  return 0;
+}
+
+struct Outcome {
+  int rc = 0;
+  uk_result r{};
+  std::string log;
+};
+
+Outcome execute(const Options& o, const std::string& hcs, const std::string& kml, const uk_plan& plan) {
+  Outcome x;
+  uk_op_desc d;
+  char err[4096];
+  uk_kml_import(kml.c_str(), &d, err, sizeof err);
+  std::vector<char> log(1 << 16);
+  x.rc = uk_run(hcs_arg(hcs), &d, &plan, o.seed, o.exact ? UK_INPUTS_EXACT : UK_INPUTS_BASELINE, o.iters, &x.r,
+                log.data(), log.size());
+  x.log = log.data();
+  return x;
+}
+
+void report(const Outcome& x, const std::string& gap) {
+  print_coverage(gap);
+  std::cout << "RUN amd:hip built=" << (x.r.built ? "yes" : "no") << " ran=" << (x.r.ran ? "yes" : "no")
+            << " verified=" << (x.r.verified ? "PASS" : "FAIL") << " max_rel=" << x.r.max_rel
+            << " measured_ms=" << x.r.measured_ms << " kernel_ms=" << x.r.kernel_ms;
+  if (x.r.migrations >= 0) std::cout << " migrations=" << x.r.migrations;
+  if (x.r.checks >= 0) std::cout << " checks=" << x.r.checks;
+  std::cout << "\n";
+  if (!x.log.empty()) {
+    constexpr size_t kTail = 1200;
+    std::cout << "-- log tail --\n" << (x.log.size() > kTail ? x.log.substr(x.log.size() - kTail) : x.log);
+    if (x.log.back() != '\n') std::cout << "\n";
+  }
+}
+
+// Violation: the migration rate over the probed allocations above the threshold, or the
+// residency refusal itself (reference include/unikern/codegen.hpp:86-91, src/main.cpp:466-471).
+bool alarm_of(const Outcome& x, double threshold, double* rate) {
+  *rate = 0;
+  bool over = false;
+  if (x.r.migrations > 0) {
+    if (x.r.checks <= 0) {
+      over = true;
+    } else {
+      *rate = double(x.r.migrations) / double(x.r.checks);
+      over = *rate > threshold;
+    }
+  }
+  return over || x.rc == UK_RESIDENCY;
+}
+
+int cmd_run(int argc, char** argv, bool write_ledger) {
+  Options o;
+  if (!parse(argc, argv, &o) || o.hcs_path.empty()) {
+    std::cerr << "usage: unikern " << (write_ledger ? "run" : "verify")
+              << " --hcs <file.json|builtin> [--ledger f] [--kml f.json | --op OP --dims D...] [--iters n] [--seed s] "
+                 "[--exact] [--migration-threshold r]\n";
+    return 2;
+  }
+  std::string hcs, kml;
+  if (!load_hcs(o, &hcs) || !load_kml(o, &kml)) return 2;
+  const std::string gap = gap_of(kml);
+  if (!gap.empty()) {
+    std::cerr << "UNSUPPORTED: " << gap << " — run/verify execute nothing and write no ledger row for this tree. "
+                 "[backend=amd:hip]\n";
+    return 2;
+  }
+  void* ledger = open_ledger(o.ledger);
+  if (!ledger) return 2;
+  uk_plan plan;
+  double c_ms = 0, m_ms = 0, k_ms = 0;
+  int32_t hit = 0;
+  if (uk_ledger_lookup(ledger, hcs_arg(hcs), kml.c_str(), &plan, &c_ms, &m_ms, &k_ms, &hit) != UK_OK) {
+    std::cerr << "ledger: " << last_error() << "\n";
+    uk_ledger_close(ledger);
+    return 2;
+  }
+  if (hit) {
+    std::cout << "LEDGER HIT  c_cached_ms=" << c_ms << "  tile=" << plan.tile_m << "x" << plan.tile_n
+              << "  plan=" << plan.key << "  (from ledger)\n";
+  } else {
+    const Solved s = solve_tree(hcs, kml);
+    if (s.rc == UK_INFEASIBLE) {
+      std::cerr << "INFEASIBLE: " << s.log << "\n";
+      uk_ledger_close(ledger);
+      return 3;
+    }
+    if (s.rc != UK_OK) {
+      std::cerr << "solve: " << s.log << "\n";
+      uk_ledger_close(ledger);
+      return 2;
+    }
+    plan = s.plan;
+  }
+  Outcome x = execute(o, hcs, kml, plan);
+  report(x, gap);
+  double rate = 0;
+  std::string used_hcs = hcs;
+  if (alarm_of(x, o.migration_threshold, &rate)) {
+    std::cout << "UNIKERN_VIOLATION what=migration_rate rate=" << rate << " threshold=" << o.migration_threshold
+              << " migrations=" << x.r.migrations << " checks=" << x.r.checks << " exit=" << x.rc
+              << " vram_free=" << x.r.vram_free << " vram_total=" << x.r.vram_total << " committed=no\n";
+    if (write_ledger)
+      uk_ledger_record_violation(ledger, hcs_arg(hcs), kml.c_str(), rate, o.migration_threshold, x.r.migrations,
+                                 x.r.checks, x.r.vram_free);
+    if (x.r.vram_free == 0) {
+      std::cerr << "RESOLVE STOP: no measured device capacity from this run; violation recorded, nothing "
+                   "committed.\n";
+      uk_ledger_close(ledger);
+      return 5;
+    }
+    std::vector<char> tight(1 << 16);
+    if (uk_hcs_with_capacity(hcs_arg(hcs), x.r.vram_free, tight.data(), tight.size()) != UK_OK) {
+      std::cerr << "RESOLVE STOP: " << last_error() << "; violation recorded, nothing committed.\n";
+      uk_ledger_close(ledger);
+      return 5;
+    }
+    used_hcs = tight.data();
+    std::cout << "RESOLVE re-solve device_capacity -> " << x.r.vram_free << " (measured by hipMemGetInfo)\n";
+    const Solved retry = solve_tree(used_hcs, kml);
+    if (retry.rc != UK_OK) {
+      std::cerr << "INFEASIBLE: " << retry.log << "\nRESOLVE INFEASIBLE at the measured capacity; nothing committed\n";
+      uk_ledger_close(ledger);
+      return 5;
+    }
+    plan = retry.plan;
+    x = execute(o, used_hcs, kml, plan);
+    report(x, gap);
+    if (alarm_of(x, o.migration_threshold, &rate)) {
+      std::cout << "UNIKERN_VIOLATION stage=retry what=migration_rate rate=" << rate << " exit=" << x.rc
+                << " committed=no\n";
+      if (write_ledger)
+        uk_ledger_record_violation(ledger, hcs_arg(used_hcs), kml.c_str(), rate, o.migration_threshold,
+                                   x.r.migrations, x.r.checks, x.r.vram_free);
+      std::cerr << "RESOLVE STOP: the retry still violates; one retry is the bound. Nothing committed.\n";
+      uk_ledger_close(ledger);
+      return 5;
+    }
+  }
+  if (!x.r.built || !x.r.ran || !x.r.verified) {
+    std::cerr << "RUN FAILED; solution NOT committed to ledger\n";
+    uk_ledger_close(ledger);
+    return x.rc == UK_OK ? 1 : x.rc;
+  }
+  if (!write_ledger) {
+    std::cout << "VERIFY PASS (no ledger write)\n";
+    uk_ledger_close(ledger);
+    return 0;
+  }
+  if (uk_ledger_commit(ledger, hcs_arg(used_hcs), kml.c_str(), &plan, x.r.measured_ms, x.r.kernel_ms) != UK_OK) {
+    std::cerr << "ledger commit failed: " << last_error() << "\n";
+    uk_ledger_close(ledger);
+    return 2;
+  }
+  const double pred = plan.predicted_us * 1e-3;
+  const double eps_abs = std::fabs(x.r.measured_ms - pred);
+  std::cout << "LEDGER COMMIT predicted_ms=" << pred << " measured_ms=" << x.r.measured_ms
+            << " kernel_ms=" << x.r.kernel_ms << " epsilon_abs=" << eps_abs
+            << " epsilon_rel=" << eps_abs / std::max(pred, 1e-9) << "\n";
+  uk_ledger_close(ledger);
+  return 0;
+}
+
+int cmd_calibrate(int argc, char** argv) {
+  Options o;
+  o.ledger.clear();
+  if (!parse(argc, argv, &o) || o.hcs_path.empty() || o.ledger.empty()) {
+    std::cerr << "usage: unikern calibrate --hcs <file.json|builtin> --ledger <l> [--out f.json]\n";
+    return 2;
+  }
+  std::string hcs;
+  if (!load_hcs(o, &hcs)) return 2;
+  void* ledger = open_ledger(o.ledger);
+  if (!ledger) return 2;
+  std::vector<char> out(1 << 16), detail(1 << 16);
+  const int rc = uk_calibrate(hcs_arg(hcs), ledger, out.data(), out.size(), detail.data(), detail.size());
+  uk_ledger_close(ledger);
+  if (rc != UK_OK) {
+    std::cerr << "CALIBRATE SKIP: " << detail.data() << "\n";
+    return 3;
+  }
+  if (o.out_path.empty()) {
+    std::cout << out.data();
+  } else {
+    std::ofstream f(o.out_path, std::ios::binary);
+    if (!(f << out.data())) {
+      std::cerr << "cannot write " << o.out_path << "\n";
+      return 2;
+    }
+  }
+  std::cout << "CALIBRATED link_bw_gbps (constants_version bumped)\n" << detail.data() << "\n";
+  return 0;
+}
+
+int cmd_backends() {
+  char arch[128] = {0};
+  const int rc = uk_device_check(arch, sizeof arch);
+  std::cout << "BACKEND amd:hip target=gfx950 abi=" << uk_abi_version()
+            << " device=" << (rc == UK_OK ? arch : "absent") << " execution=resident-only\n";
+  return 0;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  if (argc >= 2) {
+    const std::string c = argv[1];
+    if (c == "kml" && argc >= 3) return cmd_kml(argv[2]);
+    if (c == "hcs" && argc >= 3) return cmd_hcs(argv[2]);
+    if (c == "solve") return cmd_solve(argc - 2, argv + 2);
+    if (c == "run") return cmd_run(argc - 2, argv + 2, true);
+    if (c == "verify") return cmd_run(argc - 2, argv + 2, false);
+    if (c == "calibrate") return cmd_calibrate(argc - 2, argv + 2);
+    if (c == "backends") return cmd_backends();
+  }
+  std::cerr << "usage: unikern <command>\n"
+            << "  kml <file.json>\n"
+            << "  hcs <file.json|builtin>\n"
+            << "  solve --hcs f [--ledger f] [--kml f.json | --op OP --dims D...] [--selfcheck]\n"
+            << "  run --hcs f [--ledger f] [--kml f.json | --op OP --dims D...] [--iters n] [--seed s] [--exact]\n"
+            << "  verify (as run, no ledger write)\n"
+            << "  calibrate --hcs f --ledger l [--out f.json]\n"
+            << "  backends\n";
+  return 2;
+}

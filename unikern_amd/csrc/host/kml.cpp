@@ -524,3 +524,60 @@ const char* to_string(Family f) {
 }
 
 }  // namespace uk
+
+namespace uk {
+
+// Inverse of op_signature: "op:dtype:d0xd1x...[:layout][:nB:pP:sS][:cs][:epsE]". Used by
+// calibration to recover a ledger row's workload (reference src/solver.cpp:194-225 parses the
+// same way). Returns nullopt for a malformed signature.
+std::optional<KmlTree> tree_from_signature(const std::string& sig) {
+  std::vector<std::string> parts;
+  size_t p = 0;
+  while (true) {
+    const size_t c = sig.find(':', p);
+    parts.push_back(sig.substr(p, c == std::string::npos ? std::string::npos : c - p));
+    if (c == std::string::npos) break;
+    p = c + 1;
+  }
+  if (parts.size() < 3) return std::nullopt;
+  const auto op = op_from_string(parts[0]);
+  const auto dt = dtype_from_string(parts[1]);
+  if (!op || !dt) return std::nullopt;
+  KmlTree t;
+  t.op = *op;
+  t.dtype = *dt;
+  t.ndims = 0;
+  try {
+    size_t q = 0;
+    while (t.ndims < 6) {
+      const size_t x = parts[2].find('x', q);
+      size_t used = 0;
+      const std::string tok = parts[2].substr(q, x == std::string::npos ? std::string::npos : x - q);
+      const long v = std::stol(tok, &used);
+      if (used != tok.size() || v <= 0 || v > INT32_MAX) return std::nullopt;
+      t.dims[t.ndims++] = int(v);
+      if (x == std::string::npos) break;
+      q = x + 1;
+    }
+    for (size_t i = 3; i < parts.size(); ++i) {
+      const std::string& s = parts[i];
+      if (const auto l = layout_from_string(s)) t.layout = *l;
+      else if (s == "cs") t.epilogue = Epilogue::ChannelScale;
+      else if (s.size() > 1 && s[0] == 'n') t.batch = std::stoi(s.substr(1));
+      else if (s.size() > 1 && s[0] == 'p') t.pad = std::stoi(s.substr(1));
+      else if (s.size() > 1 && s[0] == 's') t.stride = std::stoi(s.substr(1));
+      else if (s.rfind("eps", 0) == 0) {
+        t.eps = std::stof(s.substr(3));
+        t.has_eps = true;
+      } else {
+        return std::nullopt;
+      }
+    }
+  } catch (...) {
+    return std::nullopt;
+  }
+  if (t.ndims < kml_arity_min(t.op) || t.ndims > kml_arity_max(t.op)) return std::nullopt;
+  return t;
+}
+
+}  // namespace uk

@@ -123,6 +123,7 @@ std::string kml_export(const KmlTree& t);
 std::string canonical_form(const KmlTree& t);
 std::string op_signature(const KmlTree& t);
 std::string fnv1a_hex(const std::string& data);
+std::optional<KmlTree> tree_from_signature(const std::string& sig);  // inverse of op_signature
 int kml_arity_min(OpKind op);
 int kml_arity_max(OpKind op);
 const char* kml_dim_spec(OpKind op);
