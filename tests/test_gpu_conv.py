@@ -80,13 +80,48 @@ def test_nchw_shapes(gpu, N, C, H, W, Oc, Kh, Kw, pad, stride):
         assert frob(y, r) <= 1e-5
 
 
-@pytest.mark.parametrize("vi", range(4))
-def test_every_conv_variant(gpu, vi):
+# Compiled conv variants (table order): 0-3 the wide kernel (any taps <= 49), 4-6 the tile
+# kernel (3x3 and 1x1 only).
+CONV_VARIANTS = 7
+TILE_VARIANTS = range(4, 7)
+
+
+@pytest.mark.parametrize("vi", range(CONV_VARIANTS))
+@pytest.mark.parametrize("shape", [(2, 40, 20, 20, 64, 3, 3, 1), (1, 3, 9, 7, 10, 3, 3, 1), (3, 32, 8, 8, 70, 1, 1, 0),
+                                   (1, 17, 6, 33, 128, 3, 3, 0)])
+def test_every_conv_variant(gpu, vi, shape):
+    # partial channel chunks, odd channel counts, Oc not a multiple of 64, several oc tiles, 1x1
+    N, C, H, W, Oc, Kh, Kw, pad = shape
     p = gpu.Plan()
     p.family, p.variant = 7, vi
-    x, w, s = rand_conv(2, 40, 20, 20, 64, 3, 3, 100 + vi)
+    x, w, s = rand_conv(N, C, H, W, Oc, Kh, Kw, 100 + vi + C)
+    y = conv_nchw_gpu(gpu, x, w, s, pad=pad, plan=p)
+    assert frob(y, O.conv_nchw(x, w, s, pad=pad)) <= 1e-5
+
+
+@pytest.mark.parametrize("vi", range(CONV_VARIANTS))
+def test_every_conv_variant_exact_and_hwc(gpu, vi):
+    p = gpu.Plan()
+    p.family, p.variant = 7, vi
+    x = O.sawtooth(2 * 24 * 15 * 15, 17, 8).reshape(2, 24, 15, 15)
+    w = O.sawtooth(64 * 24 * 9, 13, 6).reshape(64, 24, 3, 3)
+    s = O.sawtooth(64, 7, 3, bias=1.0)
     y = conv_nchw_gpu(gpu, x, w, s, pad=1, plan=p)
-    assert frob(y, O.conv_nchw(x, w, s, pad=1)) <= 1e-5
+    assert np.array_equal(y.view(np.uint32), O.conv_nchw(x, w, s, pad=1).view(np.uint32))
+    H, W, C, Kh, Kw, Oc = 12, 10, 6, 3, 3, 40
+    xh = O.normal(H * W * C, 50 + vi, 0.0, 1.0)
+    wt = O.normal(Oc * Kh * Kw * C, 60 + vi, 0.0, 0.3)
+    y = conv_hwc_gpu(gpu, xh, wt, H, W, C, Kh, Kw, Oc, plan=p)
+    assert frob(y, O.cpu_conv(xh, wt, H, W, C, Kh, Kw, Oc)) <= 1e-5
+
+
+@pytest.mark.parametrize("vi", TILE_VARIANTS)
+def test_tile_variants_refuse_other_kernel_sizes(gpu, vi):
+    p = gpu.Plan()
+    p.family, p.variant = 7, vi
+    x, w, s = rand_conv(1, 8, 11, 13, 8, 5, 5, 3)
+    with pytest.raises(gpu.UnikernError):
+        conv_nchw_gpu(gpu, x, w, s, pad=2, plan=p)
 
 
 def test_reference_sample_hwc_exact_mode(gpu):

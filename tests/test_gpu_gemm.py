@@ -12,9 +12,9 @@ import _oracle as O
 
 pytestmark = pytest.mark.gpu
 
-# (bm, bn, bk) of each compiled fast variant, in table order (unikern_amd/csrc/variants.hpp).
+# (BM, BN, BK) of every compiled f16 TN variant, in table order.
 F16_VARIANTS = [(256, 256, 32), (256, 256, 32), (256, 256, 32), (256, 256, 32), (256, 128, 32), (256, 128, 64),
-                (128, 128, 64), (128, 128, 32)]
+                (128, 128, 64), (128, 128, 32), (256, 256, 32), (256, 256, 32)]
 
 
 def gemm_gpu(uk, A, B, dtype, layout, plan=None):

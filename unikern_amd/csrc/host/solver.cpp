@@ -308,54 +308,66 @@ std::optional<Plan> solve_conv(const Hcs& h, const KmlTree& t, const Shape& s, S
   const int64_t strips = (s.Ho * s.Wo + 31) / 32;
   const int64_t units = s.Nb * strips;          // 32-pixel strips
   const int64_t oc_tiles = (s.Co + 63) / 64;
-  const int64_t waves_total = units * oc_tiles;
   const double simd_slots = double(cus(h)) * simds(h);
-  // One wavefront's reduction: two 32x32 tiles per (channel pair, tap); an MFMA 32x32x2 f32
-  // occupies the SIMD for 4096 FLOP at the per-SIMD f32 rate.
+  // One 32x32 output tile over the whole reduction: one MFMA 32x32x2 f32 per (channel pair,
+  // tap), each 4096 FLOP at the per-SIMD f32 rate.
   const double per_simd_flop_clk = peak * 1e12 / (simd_slots * clk * 1e6);
-  const double mfma_cycles = 4096.0 / per_simd_flop_clk;
-  const double wave_cycles = 2.0 * double((s.Ci + 1) / 2) * double(taps) * mfma_cycles;
+  const double tile_cycles = double((s.Ci + 1) / 2) * double(taps) * (4096.0 / per_simd_flop_clk);
   std::vector<Cand> cs;
   for (int i = 0; i < kNumConvVariants; ++i) {
     const ConvVariant v = kConvVariants[i];
     std::ostringstream key;
-    key << "conv_igemm:w" << v.waves << ",lds" << v.bk_bytes;
-    const int64_t per_channel = taps * 64 * 4;
-    int64_t cb = (v.bk_bytes / per_channel) & ~int64_t(1);
-    if (taps > 49) {
-      reject(log, key.str() + " violates taps<=49 (per-lane tap table)");
-      continue;
+    const bool tile = v.tile_strips > 0;
+    if (tile) key << "conv_tile:s" << v.tile_strips << ",cb" << v.bk_bytes;
+    else key << "conv_igemm:w" << v.waves << ",lds" << v.bk_bytes;
+    int64_t cb = 0, lds = 0, wgs = 0;
+    double tiles_per_wave = 0;
+    if (tile) {
+      if (taps != 9 && taps != 1) {
+        reject(log, key.str() + " violates taps in {9, 1} (compiled kernel sizes)");
+        continue;
+      }
+      cb = v.bk_bytes;
+      lds = cb * taps * 97 * 4;
+      wgs = ((units + v.tile_strips - 1) / v.tile_strips) * oc_tiles;
+      tiles_per_wave = 1;
+    } else {
+      if (taps > 49) {
+        reject(log, key.str() + " violates taps<=49 (per-lane tap table)");
+        continue;
+      }
+      const int64_t per_channel = taps * 64 * 4;
+      cb = (v.bk_bytes / per_channel) & ~int64_t(1);
+      if (cb < 2) {
+        reject(log, key.str() + " violates LDS budget >= 2 channels x taps x 64 oc");
+        continue;
+      }
+      cb = std::min<int64_t>(cb, (s.Ci + 1) & ~int64_t(1));
+      lds = cb * per_channel;
+      wgs = ((units + v.waves - 1) / v.waves) * oc_tiles;
+      tiles_per_wave = 2;
     }
-    if (cb < 2) {
-      reject(log, key.str() + " violates LDS budget >= 2 channels x taps x 64 oc");
-      continue;
-    }
-    if (v.bk_bytes > lds_block(h)) {
+    if (lds > lds_block(h)) {
       reject(log, key.str() + " violates LDS per workgroup");
       continue;
     }
-    cb = std::min<int64_t>(cb, (s.Ci + 1) & ~int64_t(1));
-    const int64_t lds = cb * per_channel;
-    const int64_t wgs = ((units + v.waves - 1) / v.waves) * oc_tiles;
-    const int resident = std::max(1, int(std::min<int64_t>(lds_cu(h) / lds, 8 * simds(h) / v.waves)));
-    // Wavefronts spread over CUs (workgroup granularity) and SIMDs; the busiest SIMD sets the time.
+    // Workgroups spread over the CUs; the busiest SIMD holds ceil(workgroups per CU) times
+    // waves / SIMDs wavefronts and sets the time.
     const int64_t wg_per_cu = (wgs + cus(h) - 1) / cus(h);
-    const double waves_per_simd = std::ceil(double(std::min<int64_t>(wg_per_cu, resident)) * v.waves / simds(h)) *
-                                  std::ceil(double(wg_per_cu) / resident);
-    const int64_t chunks = (s.Ci + cb - 1) / cb;
-    const double stage_us = double(chunks) * (double(lds) / 64.0 / clk + 1.0);  // per-CU L2 feed + latency
-    const double cost = launch_us(h) + waves_per_simd * wave_cycles / (clk * 0.8) + stage_us;
+    const double waves_per_simd = std::ceil(double(wg_per_cu) * v.waves / simds(h));
+    const double cost = launch_us(h) + waves_per_simd * tiles_per_wave * tile_cycles / (clk * v.eff);
     Cand c;
     c.plan.family = Family::ConvIgemm;
     c.plan.variant = i;
-    c.plan.tile_m = 64;
-    c.plan.tile_n = 32 * v.waves;
+    c.plan.tile_m = tile ? 32 : 64;
+    c.plan.tile_n = 32 * (tile ? v.tile_strips : v.waves);
     c.plan.tile_k = int(cb * taps);
     c.plan.threads = v.waves * 64;
     c.plan.grid = wgs;
     c.plan.key = key.str();
-    c.plan.why = std::to_string(waves_total) + " wavefronts over " + std::to_string(int64_t(simd_slots)) +
-                 " SIMDs, " + std::to_string(cb) + " channels per staged weight chunk";
+    c.plan.why = std::to_string(wgs) + " workgroups of " + std::to_string(v.waves) + " wavefronts, " +
+                 std::to_string(cb) + " channels per staged weight chunk, calibrated MFMA efficiency " +
+                 fmt("%.2f", v.eff);
     c.cost = cost;
     cs.push_back(c);
   }

@@ -129,7 +129,9 @@ __global__ void __launch_bounds__(WAVES * 64)
     __syncthreads();
 
     // Reduction over this chunk: channel pairs (c, c+1) outer, taps inner. Gathers use clamped
-    // addresses (always inside the input) and a select, so no load is predicated.
+    // addresses (always inside the input) and a select, so no load is predicated. The next pair's
+    // activations (global) and weights (LDS) are loaded before the current pair's MFMAs, so
+    // neither latency sits in front of the matrix pipe.
     float xv[kMaxTaps], xn[kMaxTaps];
     auto gather = [&](float (&dst)[kMaxTaps], int c) {
       const int cc = c + kk;
@@ -143,28 +145,66 @@ __global__ void __launch_bounds__(WAVES * 64)
         dst[t] = ok ? val : 0.f;
       }
     };
-    auto step = [&](int c, f32x16& acc0, f32x16& acc1) {
+    if constexpr (TAPS > 0) {
+      // Weight operands of pair c: w[t] for output channels 0-31 and 32-63 of the tile. Pairs
+      // past the chunk read channel 0's row (inside the staged chunk; their activations are 0).
+      float wv0[TAPS], wv1[TAPS], wn0[TAPS], wn1[TAPS];
+      auto wload = [&](float (&w0)[TAPS], float (&w1)[TAPS], int c) {
+        const int cc = c + kk;
+        const float* wr = wl + (cc < cn ? cc : 0) * taps * 64 + (lane & 31);
 #pragma unroll
-      for (int t = 0; t < kMaxTaps; ++t) {
-        if (t < taps) {
-          const float* wr = wl + ((c + kk) * taps + t) * 64 + (lane & 31);
-          acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(wr[0], xv[t], acc0, 0, 0, 0);
-          acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(wr[32], xv[t], acc1, 0, 0, 0);
+        for (int t = 0; t < TAPS; ++t) {
+          w0[t] = wr[t * 64];
+          w1[t] = wr[t * 64 + 32];
         }
-      }
-    };
-    gather(xv, 0);
-    for (int c = 0; c < cn; c += 4) {
-      // pair c into accumulator set 0, pair c+2 into set 1 (independent MFMA chains)
-      gather(xn, c + 2);
-      step(c, acc[0][0], acc[1][0]);
+      };
+      auto mfma_pair = [&](const float (&w0)[TAPS], const float (&w1)[TAPS], f32x16& acc0, f32x16& acc1) {
 #pragma unroll
-      for (int t = 0; t < kMaxTaps; ++t) xv[t] = xn[t];
-      if (c + 2 < cn) {
-        gather(xn, c + 4);
-        step(c + 2, acc[0][1], acc[1][1]);
+        for (int t = 0; t < TAPS; ++t) {
+          acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(w0[t], xv[t], acc0, 0, 0, 0);
+          acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(w1[t], xv[t], acc1, 0, 0, 0);
+        }
+      };
+      gather(xv, 0);
+      wload(wv0, wv1, 0);
+      for (int c = 0; c < cn; c += 4) {
+        // pair c into accumulator set 0, pair c+2 into set 1 (independent MFMA chains)
+        gather(xn, c + 2);
+        wload(wn0, wn1, c + 2);
+        mfma_pair(wv0, wv1, acc[0][0], acc[1][0]);
 #pragma unroll
         for (int t = 0; t < kMaxTaps; ++t) xv[t] = xn[t];
+        if (c + 2 < cn) {
+          gather(xn, c + 4);
+          wload(wv0, wv1, c + 4);
+          mfma_pair(wn0, wn1, acc[0][1], acc[1][1]);
+#pragma unroll
+          for (int t = 0; t < kMaxTaps; ++t) xv[t] = xn[t];
+        }
+      }
+    } else {
+      auto step = [&](int c, f32x16& acc0, f32x16& acc1) {
+#pragma unroll
+        for (int t = 0; t < kMaxTaps; ++t) {
+          if (t < taps) {
+            const float* wr = wl + ((c + kk) * taps + t) * 64 + (lane & 31);
+            acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(wr[0], xv[t], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(wr[32], xv[t], acc1, 0, 0, 0);
+          }
+        }
+      };
+      gather(xv, 0);
+      for (int c = 0; c < cn; c += 4) {
+        gather(xn, c + 2);
+        step(c, acc[0][0], acc[1][0]);
+#pragma unroll
+        for (int t = 0; t < kMaxTaps; ++t) xv[t] = xn[t];
+        if (c + 2 < cn) {
+          gather(xn, c + 4);
+          step(c + 2, acc[0][1], acc[1][1]);
+#pragma unroll
+          for (int t = 0; t < kMaxTaps; ++t) xv[t] = xn[t];
+        }
       }
     }
   }
@@ -182,6 +222,160 @@ __global__ void __launch_bounds__(WAVES * 64)
         yb[(int64_t)oc * P + p] = a.scale ? s * a.scale[oc] : s;
       }
     }
+}
+
+// ---------------------------------------------------------------------------------------
+// conv_tile_kernel: the same implicit GEMM with a wavefront per 32 pixels x 32 output channels
+// and a workgroup of S strips x 2 channel halves, so twice as many wavefronts share the SIMDs and
+// hide each other's latency. The weights stream through LDS in chunks of CB input channels,
+// loaded coalesced along each output channel's contiguous (channel, tap) row and written
+// transposed as wl[(c, tap)][oc] with an odd pitch (kPitch = 97 floats) that keeps both the
+// transposing writes and the MFMA operand reads (two channel rows 9 * 97 floats apart) nearly free
+// of bank conflicts. The next chunk's loads are in flight while the current chunk is reduced.
+// TAPS is a compile-time kernel size (9 or 1); the reduction order per output is the same as the
+// wide kernel's (channel pairs alternating between two accumulators, taps ascending).
+template <bool NCHW, int TAPS, int S, int CB>
+__global__ void __launch_bounds__(S * 2 * 64)
+    conv_tile_kernel(ConvArgs a) {
+  constexpr int kWaves = S * 2;
+  constexpr int kOcs = 64;                   // output channels per workgroup (two halves)
+  constexpr int kPitch = kOcs + 33;          // odd: conflict-free transposing writes
+  constexpr int kRow = CB * TAPS;            // (channel, tap) entries of one chunk
+  static_assert(CB % 2 == 0, "channel pairs");
+  __shared__ float wl[kRow * kPitch];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int sidx = wave >> 1, half = wave & 1;
+  const int unit = blockIdx.x * S + sidx;
+  const bool active = unit < a.N * a.strips;
+  const int n = active ? unit / a.strips : 0;
+  const int P = a.Ho * a.Wo;
+  const int p = (active ? unit % a.strips : 0) * 32 + (lane & 31);
+  const bool pvalid = active && p < P;
+  const int ho = pvalid ? p / a.Wo : 0, wo = pvalid ? p % a.Wo : 0;
+  const int kk = lane >> 5;
+  const int oc_base = blockIdx.y * kOcs;
+
+  int off[TAPS];
+#pragma unroll
+  for (int t = 0; t < TAPS; ++t) {
+    const int kh = t / a.Kw, kw = t % a.Kw;
+    const int hi = ho * a.stride + kh - a.pad, wi = wo * a.stride + kw - a.pad;
+    const bool ok = pvalid && hi >= 0 && hi < a.H && wi >= 0 && wi < a.W;
+    off[t] = ok ? (NCHW ? hi * a.W + wi : (hi * a.W + wi) * a.C) : -1;
+  }
+  const int64_t HW = (int64_t)a.H * a.W;
+  const float* xb = NCHW ? a.x + (int64_t)n * a.C * HW : a.x;
+  const int64_t cstride = NCHW ? HW : 1;
+
+  // Chunk staging: wavefront w copies output-channel rows ocl = w, w + kWaves, ...; lane l takes
+  // entries r = l + 64 q of the row, r the (channel, tap) index in the order the caller's layout
+  // stores contiguously for one output channel (NCHW/OIHW: channel-major; NT: tap-major), so a
+  // load instruction reads consecutive floats of one row and the per-lane (channel, tap) split is
+  // computed once. The LDS entry is wl[(channel * TAPS + tap) * kPitch + ocl].
+  constexpr int kRowsW = kOcs / kWaves;  // rows per wavefront
+  constexpr int kQ = (kRow + 63) / 64;   // 64-entry pieces of a row
+  static_assert(kOcs % kWaves == 0, "rows split evenly over the wavefronts");
+  int cl_q[kQ], t_q[kQ], lds_q[kQ];
+#pragma unroll
+  for (int q = 0; q < kQ; ++q) {
+    const int r = lane + 64 * q;
+    int cl, t;
+    if constexpr (NCHW) {
+      cl = r / TAPS;
+      t = r - cl * TAPS;
+    } else {
+      t = r / CB;
+      cl = r - t * CB;
+    }
+    cl_q[q] = r < kRow ? cl : CB;  // CB marks a lane past the row
+    t_q[q] = t;
+    lds_q[q] = (cl * TAPS + t) * kPitch;
+  }
+  float wreg[kRowsW][kQ];
+  auto load_chunk = [&](int c0) {
+#pragma unroll
+    for (int i = 0; i < kRowsW; ++i) {
+      const int oc = oc_base + wave + i * kWaves;
+#pragma unroll
+      for (int q = 0; q < kQ; ++q) {
+        const int c = c0 + cl_q[q];
+        const bool ok = cl_q[q] < CB && oc < a.Oc && c < a.C;
+        const int64_t gi = NCHW ? ((int64_t)oc * a.C + c) * TAPS + t_q[q] : ((int64_t)oc * TAPS + t_q[q]) * a.C + c;
+        const float v = a.w[ok ? gi : 0];
+        wreg[i][q] = ok ? v : 0.f;
+      }
+    }
+  };
+  auto store_chunk = [&]() {
+#pragma unroll
+    for (int i = 0; i < kRowsW; ++i)
+#pragma unroll
+      for (int q = 0; q < kQ; ++q)
+        if (cl_q[q] < CB) wl[lds_q[q] + wave + i * kWaves] = wreg[i][q];
+  };
+
+  f32x16 acc[2] = {f32x16{}, f32x16{}};
+  float xv[TAPS], xn[TAPS], wv[TAPS], wn[TAPS];
+  const int ocl = half * 32 + (lane & 31);
+  load_chunk(0);
+  for (int c0 = 0; c0 < a.C; c0 += CB) {
+    const int cn = (a.C - c0) < CB ? (a.C - c0) : CB;
+    __syncthreads();  // every read of the previous chunk is done
+    store_chunk();
+    __syncthreads();
+    if (c0 + CB < a.C) load_chunk(c0 + CB);  // in flight while this chunk is reduced
+
+    auto gather = [&](float (&dst)[TAPS], int c) {
+      const int cc = c + kk;
+      const bool cok = cc < cn;
+      const float* base = xb + (int64_t)(c0 + (cok ? cc : 0)) * cstride;
+#pragma unroll
+      for (int t = 0; t < TAPS; ++t) {
+        const int o = off[t];
+        const bool ok = cok && o >= 0;
+        const float v = base[ok ? o : 0];
+        dst[t] = ok ? v : 0.f;
+      }
+    };
+    auto wload = [&](float (&dst)[TAPS], int c) {
+      const int cc = c + kk;
+      const float* wr = wl + (cc < cn ? cc : 0) * TAPS * kPitch + ocl;
+#pragma unroll
+      for (int t = 0; t < TAPS; ++t) dst[t] = wr[t * kPitch];
+    };
+    gather(xv, 0);
+    wload(wv, 0);
+    for (int c = 0; c < cn; c += 2) {
+      const bool more = c + 2 < cn;
+      if (more) {
+        gather(xn, c + 2);
+        wload(wn, c + 2);
+      }
+      f32x16& ac = acc[(c >> 1) & 1];
+#pragma unroll
+      for (int t = 0; t < TAPS; ++t) ac = __builtin_amdgcn_mfma_f32_32x32x2f32(wv[t], xv[t], ac, 0, 0, 0);
+      if (more) {
+#pragma unroll
+        for (int t = 0; t < TAPS; ++t) {
+          xv[t] = xn[t];
+          wv[t] = wn[t];
+        }
+      }
+    }
+  }
+
+  // Epilogue: lane -> pixel p (column), rows oc = oc_base + 32 half + 8 (r / 4) + 4 kk + r % 4.
+  if (!pvalid) return;
+  float* yb = NCHW ? a.y + (int64_t)n * a.Oc * P : a.y;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int oc = oc_base + half * 32 + (r >> 2) * 8 + kk * 4 + (r & 3);
+    if (oc < a.Oc) {
+      const float v = acc[0][r] + acc[1][r];
+      yb[(int64_t)oc * P + p] = a.scale ? v * a.scale[oc] : v;
+    }
+  }
 }
 
 }  // namespace uk::kern
@@ -207,6 +401,25 @@ hipError_t conv_taps(const kern::ConvArgs& a, int64_t units, int oc_tiles, size_
   if (taps == 9) return conv_go<NCHW, 9, WAVES>(a, units, oc_tiles, lds, s);
   if (taps == 1) return conv_go<NCHW, 1, WAVES>(a, units, oc_tiles, lds, s);
   return conv_go<NCHW, 0, WAVES>(a, units, oc_tiles, lds, s);
+}
+}  // namespace
+
+namespace {
+template <bool NCHW, int TAPS, int S, int CB>
+hipError_t conv_tile_go(const kern::ConvArgs& a, int64_t units, int oc_tiles, hipStream_t s) {
+  const unsigned grid = (unsigned)((units + S - 1) / S);
+  hipLaunchKernelGGL((kern::conv_tile_kernel<NCHW, TAPS, S, CB>), dim3(grid, (unsigned)oc_tiles), dim3(S * 128), 0,
+                     s, a);
+  return hipGetLastError();
+}
+template <int S, int CB>
+hipError_t conv_tile_dispatch(bool nchw, int taps, const kern::ConvArgs& a, int64_t units, int oc_tiles,
+                              hipStream_t s) {
+  if (taps == 9)
+    return nchw ? conv_tile_go<true, 9, S, CB>(a, units, oc_tiles, s) : conv_tile_go<false, 9, S, CB>(a, units, oc_tiles, s);
+  if (taps == 1)
+    return nchw ? conv_tile_go<true, 1, S, CB>(a, units, oc_tiles, s) : conv_tile_go<false, 1, S, CB>(a, units, oc_tiles, s);
+  return hipErrorInvalidValue;
 }
 }  // namespace
 
@@ -239,6 +452,17 @@ hipError_t launch_conv_igemm(const Plan& p, const Shape& sh, Layout lay, const f
   a.Ho = (int)sh.Ho;
   a.Wo = (int)sh.Wo;
   a.strips = (int)((sh.Ho * sh.Wo + 31) / 32);
+  if (v.tile_strips > 0) {  // 32 x 32 wavefront tiles, chunked coalesced weight staging
+    if (taps != 9 && taps != 1) return hipErrorInvalidValue;
+    a.cb = v.bk_bytes;  // channels per chunk
+    const int64_t units = sh.Nb * a.strips;
+    const int oc_tiles = (int)((sh.Co + 63) / 64);
+    if ((units + v.tile_strips - 1) / v.tile_strips > INT32_MAX || oc_tiles > 65535) return hipErrorInvalidValue;
+    if (v.tile_strips == 2 && v.bk_bytes == 16) return conv_tile_dispatch<2, 16>(nchw, (int)taps, a, units, oc_tiles, s);
+    if (v.tile_strips == 2 && v.bk_bytes == 8) return conv_tile_dispatch<2, 8>(nchw, (int)taps, a, units, oc_tiles, s);
+    if (v.tile_strips == 4 && v.bk_bytes == 8) return conv_tile_dispatch<4, 8>(nchw, (int)taps, a, units, oc_tiles, s);
+    return hipErrorInvalidValue;
+  }
   // Channel chunk: as many (even) channels as the LDS budget of the variant allows.
   const int64_t per_channel = taps * 64 * 4;
   int64_t cb = v.bk_bytes / per_channel;

@@ -328,6 +328,7 @@ hipError_t launch_gemm_f16(const Plan& p, const void* A, const void* B, void* C,
   if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX / 2) return hipErrorInvalidValue;
   if ((((uintptr_t)A) | ((uintptr_t)B) | ((uintptr_t)C)) & 15) return hipErrorInvalidValue;
   if ((M / v.bm) * (N / v.bn) > INT32_MAX) return hipErrorInvalidValue;
+  static_assert(kNumGemmF16Variants == 10, "every GEMM variant needs a case below");
   switch (p.variant) {
 #define UK_GEMM_CASE(I) \
   case I:                 \
@@ -340,6 +341,8 @@ hipError_t launch_gemm_f16(const Plan& p, const void* A, const void* B, void* C,
     UK_GEMM_CASE(5)
     UK_GEMM_CASE(6)
     UK_GEMM_CASE(7)
+    UK_GEMM_CASE(8)
+    UK_GEMM_CASE(9)
 #undef UK_GEMM_CASE
     default: return hipErrorInvalidValue;
   }

@@ -44,6 +44,8 @@ constexpr GemmF16Variant kGemmF16Variants[] = {
     {256, 128, 64, 2, 2, 3, 1, 0.307},
     {128, 128, 64, 2, 2, 3, 1, 0.223},
     {128, 128, 32, 2, 2, 4, 2, 0.280},
+    {256, 256, 32, 2, 4, 5, 2, 0.380},
+    {256, 256, 32, 2, 2, 5, 2, 0.340},
 };
 constexpr int kNumGemmF16Variants = sizeof(kGemmF16Variants) / sizeof(kGemmF16Variants[0]);
 
@@ -62,18 +64,22 @@ constexpr Q8Variant kQ8Variants[] = {{16, 4, 4, 0}, {16, 4, 1, 0}, {8, 8, 4, 0},
                                      {8, 4, 4, 1},  {4, 4, 4, 1},  {4, 8, 4, 1}};
 constexpr int kNumQ8Variants = sizeof(kQ8Variants) / sizeof(kQ8Variants[0]);
 
-// Implicit-GEMM conv on f32 MFMA (v_mfma_f32_32x32x2f32): a wavefront owns 32 output pixels x
-// 64 output channels; waves per workgroup, and the LDS budget for one staged weight chunk
-// (channels per chunk = budget / (taps * 64 * 4 B), even).
+// Implicit-GEMM conv on f32 MFMA (v_mfma_f32_32x32x2f32). Wide kernel (tile_strips 0): a
+// wavefront owns 32 output pixels x 64 output channels, `waves` wavefronts per workgroup, and
+// bk_bytes is the LDS budget of one staged weight chunk (channels = budget / (taps * 64 * 4 B),
+// even). Tile kernel (tile_strips S > 0, 3x3 and 1x1 only): wavefronts of 32 pixels x 32 output
+// channels, S strips x 2 channel halves per workgroup, bk_bytes channels per weight chunk. eff is
+// the calibrated fraction of the f32 MFMA rate the busiest SIMD sustains (kernel-only median at
+// the BASELINE conv shape on one MI355X).
 struct ConvVariant {
   int waves;
   int bk_bytes;
+  int tile_strips;
+  double eff;
 };
 constexpr ConvVariant kConvVariants[] = {
-    {4, 147456},
-    {2, 73728},
-    {4, 73728},
-    {2, 36864},
+    {4, 147456, 0, 0.273}, {2, 73728, 0, 0.175}, {4, 73728, 0, 0.260}, {2, 36864, 0, 0.170},
+    {4, 16, 2, 0.130},     {4, 8, 2, 0.130},     {8, 8, 4, 0.310},
 };
 constexpr int kNumConvVariants = sizeof(kConvVariants) / sizeof(kConvVariants[0]);
 
