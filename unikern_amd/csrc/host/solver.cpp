@@ -282,7 +282,14 @@ std::optional<Plan> solve_q8(const Hcs& h, const KmlTree& t, const Shape& s, Sol
     const double inflight = double(per_round) * 16.0 * 68.0 * useful * (v.db && rounds > 1 ? 2.0 : 1.0);
     // Copy instructions: 16-byte copies issue a quarter of the dword ones.
     const double issue_us = double(rounds) * (v.vec == 4 ? 0.3 : 1.2);
-    const double cost = launch_us(h) + stream_us(h, double(w.bytes) / useful, grid, resident, inflight) + issue_us;
+    // Each generation of resident workgroups waits one load latency before its first round
+    // lands and folds its split-K partials after its last; nothing overlaps those within a
+    // generation (fitted: about 1 us per generation over the variants at N = 11008).
+    const int64_t slots = int64_t(cus(h)) * resident;
+    const int64_t generations = (grid + slots - 1) / slots;
+    const double gen_us = double(generations) * 0.5 * kMemLatencyUs;
+    const double cost =
+        launch_us(h) + stream_us(h, double(w.bytes) / useful, grid, resident, inflight) + issue_us + gen_us;
     Cand c;
     c.plan.family = Family::Q8Gemm;
     c.plan.variant = i;
