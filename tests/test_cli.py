@@ -17,7 +17,7 @@ SAMPLES = ROOT / "samples"
 
 
 def cli(uk, *args, cwd=None, timeout=300):
-    assert uk.CLI.exists(), "the CLI is built with the library (python -m unikern_amd.build)"
+    assert uk.CLI.exists(), "the CLI is built with the library (python3 unikern_amd/build.py)"
     p = subprocess.run([str(uk.CLI), *map(str, args)], capture_output=True, text=True, cwd=cwd, timeout=timeout)
     return p.returncode, p.stdout, p.stderr
 

@@ -113,7 +113,7 @@ def load(path: Path | str = LIB_PATH) -> C.CDLL:
     p = Path(path)
     if not p.exists():
         raise ImportError(
-            f"{p} is missing: build it with `python -m unikern_amd.build` (or __graft_entry__.build()); "
+            f"{p} is missing: build it with `python3 unikern_amd/build.py` (or __graft_entry__.build()); "
             "the MI355X kernels have no fallback path")
     lib = C.CDLL(str(p))
     for name, (args, res) in _SIG.items():

@@ -4,7 +4,10 @@ Host C++ (front end, solver, inputs, self-check) is compiled with g++; HIP sourc
 the C ABI) with hipcc --offload-arch=gfx950. Objects go to unikern_amd/_build/ and the shared
 library to unikern_amd/libunikern_hip.so, in-tree, so it travels with the repository snapshot.
 
-Usage: python -m unikern_amd.build   (or unikern_amd.build.build())
+Usage: python3 unikern_amd/build.py
+
+Run it by path: `python -m unikern_amd.build` imports the package first, and the package loads
+the library this script builds, so it fails whenever that library is missing or stale.
 """
 from __future__ import annotations
 

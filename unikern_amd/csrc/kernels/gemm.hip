@@ -7,13 +7,18 @@
 //   (column-major B: both operands K-contiguous), f32 accumulate in v_mfma_f32_32x32x16_f16.
 //   * BM x BN x BK macro tile per workgroup, WM x WN wavefronts, each a (BM/WM) x (BN/WN)
 //     block of 32x32 MFMA tiles with accumulators resident in AGPR/VGPR.
-//   * global -> LDS with global_load_lds_dwordx4 (no VGPR staging): one instruction moves
-//     8 rows x 128 B into 1 KiB of LDS; the 16-byte chunk index is XOR-swizzled by row on the
-//     global side, so the MFMA fragment reads (ds_read_b128, 32 rows at one k offset) hit
-//     distinct banks.
+//   * global -> LDS with buffer_load_dwordx4 ... lds (no VGPR staging): one instruction moves
+//     1 KiB (16 rows x 64 B at BK = 32) into LDS. The buffer form takes a scalar resource and
+//     one 32-bit offset per lane, which keeps the texture addresser's queues short (the 64-bit
+//     per-lane global form backed them up and stalled the issuing wave); the resource's record
+//     count covers exactly the tile's rows, so no offset can reach past the operand. The
+//     16-byte chunk index is XOR-swizzled by row on the global side, so the MFMA fragment reads
+//     (ds_read_b128, 32 rows at one k offset) hit distinct banks.
 //   * STAGES-deep LDS ring (4 x 32 KiB for 256x256x32): the DMA runs STAGES-1 k-tiles ahead,
-//     with partial vmcnt waits, and one barrier per k-tile; MFMA fragments are double
-//     buffered in registers so LDS reads for the next k-step overlap the current MFMAs.
+//     with partial vmcnt waits, and one barrier per k-tile. Each k-step issues its share of the
+//     next tile's copies, spread evenly between the MFMAs (a burst at the start of the tile
+//     filled the addresser's queues); MFMA fragments are double buffered in registers so LDS
+//     reads for the next k-step overlap the current MFMAs.
 //   * workgroup -> tile mapping is XCD-aware: workgroup i runs on XCD i % 8, so ids are
 //     regrouped so each XCD owns a compact block of tiles and shares A/B panels in its L2.
 //   * the MFMA computes C^T tiles (B fragment as the first operand), so each lane holds four
@@ -47,6 +52,7 @@ struct GemmF16Cfg {
   static constexpr int kInstsA = BM / kRowsPerInst / kWaves;  // DMA instructions per wave per k-tile
   static constexpr int kInstsB = BN / kRowsPerInst / kWaves;
   static constexpr int kInsts = kInstsA + kInstsB;
+  static constexpr int kInstsPerStep = kInsts / kKK;  // copies issued per k-step
   static constexpr int kPitch = kWTN * 2 + 16;  // epilogue staging row pitch (bytes)
   static constexpr int kEpiBytes = kWaves * kWTM * kPitch;
   static constexpr int kLdsBytes = (STAGES * kStageBytes > kEpiBytes) ? STAGES * kStageBytes : kEpiBytes;
@@ -57,7 +63,30 @@ struct GemmF16Cfg {
                 "DMA instructions must split evenly over the wavefronts");
   static_assert(STAGES >= 3, "the ring prefetches at least two k-tiles ahead");
   static_assert((STAGES - 2) * kInsts <= 63, "outstanding DMA must fit the vmcnt counter");
+  static_assert(kInsts % kKK == 0, "copies must split evenly over the k-steps");
 };
+
+// One 1 KiB copy to LDS: lane offset voff and scalar offset soff (bytes) into the buffer of
+// nbytes at base; offsets at or past nbytes read zero. A plain device function: the resource
+// type is device-only, and kernel-template lambdas that name it lose their host launch stub.
+__device__ __forceinline__ void copy_to_lds(const void* base, int nbytes, char* dst, int voff, int soff) {
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, nbytes, 0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)dst, 16, voff, soff, 0, 0);
+}
+
+// Scheduling pattern of one k-step: NM MFMAs with NR LDS reads and ND copies spread evenly
+// between them (after MFMA m: the reads and copies whose even share falls due there).
+template <int NM, int NR, int ND, int M = 0>
+__device__ __forceinline__ void sched_spread() {
+  if constexpr (M < NM) {
+    constexpr int dr = ((M + 1) * NR + NM - 1) / NM - (M * NR + NM - 1) / NM;
+    constexpr int dv = ((M + 1) * ND) / NM - (M * ND) / NM;
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+    if constexpr (dr > 0) __builtin_amdgcn_sched_group_barrier(0x100, dr, 0);  // DS reads
+    if constexpr (dv > 0) __builtin_amdgcn_sched_group_barrier(0x020, dv, 0);  // VMEM (copies)
+    sched_spread<NM, NR, ND, M + 1>();
+  }
+}
 
 // Physical 16-byte chunk of logical chunk c in LDS row r: c ^ f(r). SWZ picks f for the bank
 // geometry (0: r, 1: r >> 1, 2: r >> 2, each masked to the chunk count).
@@ -74,27 +103,6 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N <= 63, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-// Issue the DMA for a ROWS x BK tile starting at g (row pitch ld elements) into LDS dst:
-// instruction i of this wave moves 1 KiB = kRowsPerInst rows; lane l fills physical chunk
-// l % kChunks of row l / kChunks, fetching the logical chunk that lands there.
-template <int ROWS, int BK, int WAVES, int SWZ>
-__device__ __forceinline__ void dma_tile(const _Float16* __restrict__ g, int64_t ld, char* dst, int wave, int lane) {
-  constexpr int kRowBytes = BK * 2;
-  constexpr int kChunks = kRowBytes / 16;
-  constexpr int kRowsPerInst = 1024 / kRowBytes;
-  constexpr int kInsts = ROWS / kRowsPerInst;
-  const int rr = lane / kChunks;
-  const int p = lane % kChunks;
-  const int w = __builtin_amdgcn_readfirstlane(wave);
-#pragma unroll
-  for (int t = 0; t < kInsts / WAVES; ++t) {
-    const int ins = t * WAVES + w;
-    const int r = ins * kRowsPerInst + rr;
-    const int c = p ^ swz<SWZ, kChunks>(r);
-    __builtin_amdgcn_global_load_lds(g + (int64_t)r * ld + c * 8, (lds_void*)(dst + ins * 1024), 16, 0, 0);
-  }
 }
 
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, int SWZ>
@@ -133,14 +141,36 @@ __global__ void __launch_bounds__(WM* WN * 64, 1)
 #pragma unroll
     for (int j = 0; j < Cfg::kFN; ++j) acc[i][j] = f32x16{};
 
-  // DMA of k-tile t into its ring slot. The tile index is clamped to the last tile, so the
-  // ring is issued without branches: a clamped issue refills a slot nobody reads again.
+  // Copies of one k-tile: this wave's instruction q (q < kInstsA: A, else B) is copy
+  // ins = (q mod kInstsA) * kWaves + w, which moves rows ins * kRowsPerInst + l / kChunks of the
+  // operand's row block (lane l fills physical chunk l % kChunks, fetching the logical chunk
+  // that lands there). The row term is a wave-uniform scalar offset. The swizzle term depends
+  // on the row only through ins modulo kPeriod, and kPeriod divides kWaves, so it is the same
+  // for every copy of this wave: one lane offset serves them all.
+  constexpr int kPeriod = (Cfg::kChunks == 4 || SWZ == 0) ? 1 : (SWZ == 1 ? 2 : 4);
+  static_assert(Cfg::kWaves % kPeriod == 0, "the swizzle period must divide the wave count");
+  const int w = __builtin_amdgcn_readfirstlane(wave);
+  const int vrow = lane / Cfg::kChunks;
+  const int vchunk = (lane % Cfg::kChunks) ^ swz<SWZ, Cfg::kChunks>((w % kPeriod) * Cfg::kRowsPerInst + vrow);
+  const int voff = (vrow * K + vchunk * 8) * 2;
+  // Copies [part * kInstsPerStep, (part + 1) * kInstsPerStep) of k-tile t into its ring slot.
+  // The tile index is clamped to the last tile, so the ring is issued without branches: a
+  // clamped issue refills a slot nobody reads again.
   const int KT = K / BK;
-  auto issue = [&](int t) {
+  auto issue = [&](int t, int part) {
     char* st = lds + (t % STAGES) * Cfg::kStageBytes;
     const int tc = t < KT ? t : KT - 1;
-    dma_tile<BM, BK, Cfg::kWaves, SWZ>(Ag + (int64_t)tc * BK, K, st, wave, lane);
-    dma_tile<BN, BK, Cfg::kWaves, SWZ>(Bg + (int64_t)tc * BK, K, st + BM * Cfg::kRowBytes, wave, lane);
+#pragma unroll
+    for (int u = 0; u < Cfg::kInstsPerStep; ++u) {
+      const int q = part * Cfg::kInstsPerStep + u;
+      const bool isA = q < Cfg::kInstsA;
+      const int ins = (isA ? q : q - Cfg::kInstsA) * Cfg::kWaves + w;
+      const int so = (ins * Cfg::kRowsPerInst * K + tc * BK) * 2;
+      if (isA)
+        copy_to_lds(Ag, BM * K * 2, st + ins * 1024, voff, so);
+      else
+        copy_to_lds(Bg, BN * K * 2, st + BM * Cfg::kRowBytes + ins * 1024, voff, so);
+    }
   };
 
   // Fragment registers, double buffered across k-steps (and across k-tiles).
@@ -174,7 +204,9 @@ __global__ void __launch_bounds__(WM* WN * 64, 1)
 
   // Prologue: tiles 0 .. STAGES-2 in flight; wait for tile 0 only.
 #pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s) issue(s);
+  for (int s = 0; s < STAGES - 1; ++s)
+#pragma unroll
+    for (int part = 0; part < Cfg::kKK; ++part) issue(s, part);
   wait_vmcnt<(STAGES - 2) * Cfg::kInsts>();
   __syncthreads();
   load_frags(fa[0], fb[0], 0, 0);
@@ -194,23 +226,11 @@ __global__ void __launch_bounds__(WM* WN * 64, 1)
         load_frags(fa[cur ^ 1], fb[cur ^ 1], kt, kk + 1);
       else
         load_frags(fa[cur ^ 1], fb[cur ^ 1], kt + 1 < KT ? kt + 1 : kt, 0);
-      if (kk == 0) issue(kt + STAGES - 1);
+      issue(kt + STAGES - 1, kk);
       mfmas(fa[cur], fb[cur]);
-      // Spread the LDS reads (and on the first step the DMA) between the MFMAs so the matrix
-      // pipe never drains while they issue.
-      if (kk == 0) {
-#pragma unroll
-        for (int q = 0; q < Cfg::kInsts; ++q) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // 1 VMEM read (DMA)
-        }
-      }
-#pragma unroll
-      for (int q = 0; q < kReadsPerStep; ++q) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, kMfmaPerStep, 0);
+      // Spread the LDS reads and this step's copies between the MFMAs so the matrix pipe
+      // never drains while they issue.
+      sched_spread<kMfmaPerStep, kReadsPerStep, Cfg::kInstsPerStep>();
     }
   }
   wait_vmcnt<0>();  // clamped refills still in flight must land before LDS is reused
@@ -326,6 +346,8 @@ hipError_t launch_gemm_f16(const Plan& p, const void* A, const void* B, void* C,
   // chunks of K-contiguous rows.
   if (M <= 0 || N <= 0 || K <= 0 || M % v.bm || N % v.bn || K % v.bk) return hipErrorInvalidValue;
   if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX / 2) return hipErrorInvalidValue;
+  // Copy offsets are 32-bit byte offsets within a row block of the operand.
+  if (int64_t(v.bm > v.bn ? v.bm : v.bn) * K * 2 > INT32_MAX) return hipErrorInvalidValue;
   if ((((uintptr_t)A) | ((uintptr_t)B) | ((uintptr_t)C)) & 15) return hipErrorInvalidValue;
   if ((M / v.bm) * (N / v.bn) > INT32_MAX) return hipErrorInvalidValue;
   static_assert(kNumGemmF16Variants == 10, "every GEMM variant needs a case below");

@@ -36,16 +36,16 @@ struct GemmF16Variant {
   double eff;
 };
 constexpr GemmF16Variant kGemmF16Variants[] = {
-    {256, 256, 32, 2, 2, 4, 1, 0.325},
-    {256, 256, 32, 2, 2, 4, 2, 0.349},
-    {256, 256, 32, 2, 2, 4, 0, 0.333},
-    {256, 256, 32, 2, 4, 4, 2, 0.388},
-    {256, 128, 32, 2, 2, 4, 2, 0.311},
-    {256, 128, 64, 2, 2, 3, 1, 0.307},
-    {128, 128, 64, 2, 2, 3, 1, 0.223},
+    {256, 256, 32, 2, 2, 4, 1, 0.371},
+    {256, 256, 32, 2, 2, 4, 2, 0.389},
+    {256, 256, 32, 2, 2, 4, 0, 0.402},
+    {256, 256, 32, 2, 4, 4, 2, 0.409},
+    {256, 128, 32, 2, 2, 4, 2, 0.326},
+    {256, 128, 64, 2, 2, 3, 1, 0.316},
+    {128, 128, 64, 2, 2, 3, 1, 0.229},
     {128, 128, 32, 2, 2, 4, 2, 0.280},
-    {256, 256, 32, 2, 4, 5, 2, 0.380},
-    {256, 256, 32, 2, 2, 5, 2, 0.340},
+    {256, 256, 32, 2, 4, 5, 2, 0.408},
+    {256, 256, 32, 2, 2, 5, 2, 0.399},
 };
 constexpr int kNumGemmF16Variants = sizeof(kGemmF16Variants) / sizeof(kGemmF16Variants[0]);
 
