@@ -9,6 +9,8 @@ every launch reads memory not touched for > 512 MiB of traffic (twice the 256 Mi
 
 Timed region: barrier (device synchronize), K steps enqueued kernel by kernel (K row-sums,
 K RMSNorms, K softmaxes, each segment between HIP events on the launch stream), synchronize.
+Before each segment's W warm-up steps the kernel runs untimed for ~50 ms of device time so the
+clocks have settled (see _settle).
 value = algorithmic bytes of K steps / event time of the K steps. Per-kernel averages feed the
 roofline of the dominant kernel. The f16 GEMM 4096^3 is timed the same way and
 reported under "secondary" (TFLOP/s and fraction of the dense f16 MFMA peak), with the conv2d
@@ -60,6 +62,27 @@ def _elapsed(uk, e0, e1) -> float:
     ms = C.c_float()
     uk._check(uk.lib.uk_event_elapsed_ms(e0, e1, C.byref(ms)))
     return float(ms.value)
+
+
+SETTLE_MS = 50.0
+
+
+def _settle(uk, d, plan, in_sets, n_in, out_sets, stream):
+    """Run the kernel back to back for about SETTLE_MS of device time before its warm-up steps.
+
+    The MI355X raises its engine and fabric clocks over several milliseconds of sustained load:
+    a 4096^3 GEMM timed right after an idle gap runs 10-15% slower for its first ~2 ms, and the
+    row kernels 2-4% slower. Settling first makes every timed segment a steady-state figure,
+    which is what a serving loop sees. Nothing here is timed or counted."""
+    e0, e1 = _events(uk)
+    uk._check(uk.lib.uk_event_record(e0, stream))
+    _launch_n(uk, d, plan, in_sets, n_in, out_sets, 5, stream)
+    uk._check(uk.lib.uk_event_record(e1, stream))
+    uk._check(uk.lib.uk_stream_synchronize(stream))
+    est = max(_elapsed(uk, e0, e1) / 5, 1e-3)
+    for e in (e0, e1):
+        uk.lib.uk_event_destroy(e)
+    _launch_n(uk, d, plan, in_sets, n_in, out_sets, int(min(20000, SETTLE_MS / est)), stream)
 
 
 def _host(uk, fill, n, seed, a, b):
@@ -115,6 +138,7 @@ def bench_rows(uk, O, steps: int, warmup: int, stream):
     for name, (d, ins, n_in, outs, nbytes) in ops.items():
         sol = uk.solve(d)
         flat = [p for s in ins for p in s]
+        _settle(uk, d, sol.plan, flat, n_in, outs, stream)
         if warmup:
             _launch_n(uk, d, sol.plan, flat, n_in, outs, warmup, stream)
         uk._check(uk.lib.uk_event_record(e0, stream))
@@ -149,6 +173,7 @@ def _time_op(uk, d, host_inputs, out_bytes, steps, warmup, stream, min_set_bytes
     optr = [o.ptr.value for o in outs]
     _launch_n(uk, d, sol.plan, flat[:n_in], n_in, optr[:1], 1, stream)
     uk._check(uk.lib.uk_stream_synchronize(stream))
+    _settle(uk, d, sol.plan, flat, n_in, optr, stream)
     e0, e1 = _events(uk)
     if warmup:
         _launch_n(uk, d, sol.plan, flat, n_in, optr, warmup, stream)

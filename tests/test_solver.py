@@ -101,22 +101,36 @@ def test_argmin_is_deterministic_under_candidate_ties(uk):
     a = uk.solve(d, hcs(device="renamed"))
     b = uk.solve(d)
     assert (a.key, a.predicted_us) == (b.key, b.predicted_us)
-    capped = hcs(hbm_bw_gbps=100)  # every candidate hits the same bandwidth cap
+    # At C = 256 only the uncalibrated 64-thread variants hold a row, both one row per wavefront
+    # in 256-thread workgroups: under a 100 GB/s cap they price identically.
+    d = uk.make_desc("rmsnorm", [4096, 256])
+    keys = _feasible_rows_keys(d)
+    assert keys == ["rows:tpr=64,nv=1", "rows:tpr=64,nv=2"]
+    capped = hcs(hbm_bw_gbps=100)
     s = uk.solve(d, capped)
-    # the non-temporal variants share the higher cap: they form the tie group
-    assert s.key == min(k for k in _feasible_rows_keys(d) if k.endswith(",nt"))
+    assert s.key == min(keys)
+    assert s.plan.variant == 0
+
+
+def test_calibrated_rows_picks(uk):
+    # The per-op efficiencies measured at 4096 x 4096 decide: the non-temporal 512-thread variant
+    # for row-sum and softmax, the two-row walking variant for RMSNorm.
+    picks = {op: uk.solve(uk.make_desc(op, [4096, 4096])).key for op in ("reduce", "rmsnorm", "softmax")}
+    assert picks == {"reduce": "rows:tpr=512,nv=2,nt", "rmsnorm": "rows:tpr=256,nv=4,nt,rpb=2",
+                     "softmax": "rows:tpr=512,nv=2,nt"}
 
 
 def _feasible_rows_keys(d):
     out = []
-    for tpr, nv, nt in [(64, 1, 0), (64, 2, 0), (64, 4, 0), (64, 8, 0), (64, 16, 0), (128, 4, 0), (128, 8, 0),
-                        (256, 1, 0), (256, 2, 0), (256, 4, 0), (256, 8, 0), (512, 2, 0), (512, 4, 0), (1024, 1, 0),
-                        (1024, 2, 0), (1024, 4, 0), (256, 4, 1), (512, 2, 1), (1024, 1, 1), (512, 4, 1),
-                        (1024, 2, 1)]:
+    for tpr, nv, nt, rpb in [(64, 1, 0, 1), (64, 2, 0, 1), (64, 4, 0, 1), (64, 8, 0, 1), (64, 16, 0, 1),
+                             (128, 4, 0, 1), (128, 8, 0, 1), (256, 1, 0, 1), (256, 2, 0, 1), (256, 4, 0, 1),
+                             (256, 8, 0, 1), (512, 2, 0, 1), (512, 4, 0, 1), (1024, 1, 0, 1), (1024, 2, 0, 1),
+                             (1024, 4, 0, 1), (256, 4, 1, 1), (512, 2, 1, 1), (1024, 1, 1, 1), (512, 4, 1, 1),
+                             (1024, 2, 1, 1), (128, 8, 1, 1), (256, 4, 1, 2), (512, 2, 1, 2)]:
         cap = tpr * nv * 4
         C = d.dims[1]
         if C % 4 == 0 and C <= cap and not (cap >= 4 * C and cap > 256):
-            out.append(f"rows:tpr={tpr},nv={nv}" + (",nt" if nt else ""))
+            out.append(f"rows:tpr={tpr},nv={nv}" + (",nt" if nt else "") + (f",rpb={rpb}" if rpb > 1 else ""))
     return out
 
 

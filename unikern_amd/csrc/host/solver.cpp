@@ -69,15 +69,17 @@ int waves_by_regs(const Hcs& h, int regs) {
 // outstanding, with at most `resident_per_cu` workgroups per CU (Little's law: sustained
 // bandwidth = bytes in flight / latency, capped at the sustainable peak).
 double stream_us(const Hcs& h, double bytes, int64_t grid, int resident_per_cu, double inflight_wg,
-                 bool nontemporal = false) {
-  const double peak = hbm_gbps(h) * 1e3 * (nontemporal ? kStreamEffNt : kStreamEff);  // bytes per microsecond
+                 bool nontemporal = false, double calibrated_eff = 0.0) {
+  const double eff = calibrated_eff > 0 ? calibrated_eff : (nontemporal ? kStreamEffNt : kStreamEff);
+  const double peak = hbm_gbps(h) * 1e3 * eff;  // bytes per microsecond
   const int64_t slots = int64_t(cus(h)) * std::max(resident_per_cu, 1);
   const int64_t active = std::min(slots, std::max<int64_t>(grid, 1));
   const double bw = std::min(peak, double(active) * inflight_wg / kMemLatencyUs);
   // Workgroups that retire while others load let reads and writes overlap; a grid that fits in
   // one round of resident workgroups loads everything first and writes everything last.
   const double rounds = double(std::max<int64_t>(grid, 1)) / double(slots);
-  const double overlap = 1.0 - 0.08 / std::max(rounds, 1.0);
+  // A calibrated efficiency was measured on a full grid and already carries this effect.
+  const double overlap = calibrated_eff > 0 ? 1.0 : 1.0 - 0.08 / std::max(rounds, 1.0);
   return bytes / (bw * overlap);
 }
 
@@ -111,6 +113,7 @@ std::optional<Plan> solve_rows(const Hcs& h, const KmlTree& t, const Shape& s, S
     const int64_t cap = int64_t(v.tpr) * v.nv * 4;
     std::ostringstream key;
     key << "rows:tpr=" << v.tpr << ",nv=" << v.nv << (v.nt ? ",nt" : "");
+    if (v.rpb > 1) key << ",rpb=" << v.rpb;
     if (s.C % 4 != 0) {
       reject(log, key.str() + " violates C%4==0 (float4 rows), C=" + std::to_string(s.C));
       continue;
@@ -124,9 +127,9 @@ std::optional<Plan> solve_rows(const Hcs& h, const KmlTree& t, const Shape& s, S
       continue;
     }
     const int wg = std::max(v.tpr, 256);
-    const int rows_per_wg = wg / v.tpr;
+    const int rows_per_wg = wg / v.tpr * v.rpb;
     const int64_t grid = (s.L + rows_per_wg - 1) / rows_per_wg;
-    const int regs = v.nv * 4 * (rms ? 2 : 1) + 24;
+    const int regs = v.nv * 4 * ((rms ? 1 : 0) + (v.rpb > 1 ? 2 : 1)) + 24;
     const int wps = waves_by_regs(h, regs);
     if (wps == 0) {
       reject(log, key.str() + " violates register budget");
@@ -134,8 +137,10 @@ std::optional<Plan> solve_rows(const Hcs& h, const KmlTree& t, const Shape& s, S
     }
     const int resident = std::max(1, (wps * simds(h)) / (wg / 64));
     const double useful = double(s.C) / double(cap);
-    const double inflight = double(wg) * v.nv * 16.0 * useful;
-    double cost = launch_us(h) + stream_us(h, double(w.bytes), grid, resident, inflight, v.nt != 0);
+    // A walking workgroup keeps its next row in flight while it reduces the current one.
+    const double inflight = double(wg) * v.nv * 16.0 * useful * (v.rpb > 1 ? 1.5 : 1.0);
+    const double eff = t.op == OpKind::Softmax ? v.eff_softmax : (rms ? v.eff_rms : v.eff_sum);
+    double cost = launch_us(h) + stream_us(h, double(w.bytes), grid, resident, inflight, v.nt != 0, eff);
     Cand c;
     c.plan.family = Family::Rows;
     c.plan.variant = i;

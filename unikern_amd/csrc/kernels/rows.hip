@@ -11,7 +11,9 @@
 //
 // Semantics kept from the reference CPU loops: rmsnorm y = (x * rms) * W with
 // rms = 1/sqrt(sum(x^2)/C + eps) (correctly rounded divide and sqrt); softmax
-// y = exp(x - max) / sum(exp(x - max)) with an IEEE divide.
+// y = exp(x - max) / sum(exp(x - max)), here as exp(x - max) * (1 / sum) with a 1.23-ulp exp:
+// within a few roundings of the reference, far inside the 1e-5 relative gate, and half the
+// vector instructions of a libm exp and a divide per element (those did not hide behind HBM).
 #include <math.h>
 
 #include "../launch.hpp"
@@ -32,36 +34,55 @@ __device__ __forceinline__ void st4(f32x4* p, f32x4 v) {
   else *p = v;
 }
 
-template <int TPR, int NV, int OP, bool NT>
+// e^d for the softmax numerators: 2^(d log2 e) on v_exp_f32, with the rounding error of the
+// product d * log2(e) (recovered exactly by an fma) and the tail of log2(e) folded back in as
+// 2^p * (1 + err * ln 2). Measured against binary64 on the device: at most 1.23 ulp over the
+// normal range d in [-87.3, 0]; e^-inf = 0; NaN propagates. libm's expf costs about three
+// times the instructions, which the softmax kernel cannot hide behind its HBM stream.
+__device__ __forceinline__ float exp_softmax(float d) {
+  constexpr float kLog2e = 1.44269502f;          // log2(e) rounded to binary32
+  constexpr float kLog2eTail = 1.925963033e-8f;  // log2(e) - kLog2e
+  constexpr float kLn2 = 0.693147181f;
+  const float p = d * kLog2e;
+  const float err = fmaf(d, kLog2eTail, fmaf(d, kLog2e, -p));
+  const float r = __builtin_amdgcn_exp2f(p);
+  return (r == 0.f) ? 0.f : fmaf(r, err * kLn2, r);
+}
+
+// TPR threads own one row at a time and each keeps NV float4 of it in registers; a workgroup
+// walks RPB rows (RPB > 1: the next row's loads are issued before the current row's reduction,
+// so the reduction's latency hides behind HBM traffic). Rows beyond L are masked, never
+// skipped: every thread reaches every barrier.
+template <int TPR, int NV, int OP, bool NT, int RPB>
 __global__ void __launch_bounds__(TPR < 256 ? 256 : TPR)
     rows_kernel(const float* __restrict__ X, const float* __restrict__ Wg, float* __restrict__ Y, int L, int C,
                 float eps) {
   constexpr int WG = TPR < 256 ? 256 : TPR;
-  constexpr int RPW = WG / TPR;  // rows per workgroup
+  constexpr int RPW = WG / TPR;  // rows per workgroup at a time
   constexpr int WPR = TPR / 64;  // wavefronts per row
-  __shared__ float red0[WG / 64];
-  __shared__ float red1[WG / 64];
+  // Reduction slots, alternating between consecutive rows: a fast wavefront may publish row
+  // k+1's partial while a slow one still reads row k's.
+  __shared__ float red0[2][WG / 64];
+  __shared__ float red1[2][WG / 64];
 
   const int tid = threadIdx.x;
   const int rloc = tid / TPR;
   const int t = tid % TPR;
   const int wave = tid >> 6;
-  const int64_t row = (int64_t)blockIdx.x * RPW + rloc;
-  const bool active = row < L;
   const int C4 = C >> 2;
-  const f32x4* x4 = reinterpret_cast<const f32x4*>(X + (active ? row : 0) * (int64_t)C);
+  auto row_of = [&](int k) -> int64_t { return ((int64_t)blockIdx.x * RPB + k) * RPW + rloc; };
 
   const float fill = (OP == 2) ? -INFINITY : 0.f;
-  f32x4 v[NV];
+  auto load_row = [&](f32x4 (&v)[NV], int k) {
+    const int64_t row = row_of(k);
+    const bool active = row < L;
+    const f32x4* x4 = reinterpret_cast<const f32x4*>(X + (active ? row : 0) * (int64_t)C);
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int j = i * TPR + t;
-    if (active && j < C4) {
-      v[i] = ld4<NT>(x4 + j);
-    } else {
-      v[i] = f32x4{fill, fill, fill, fill};
+    for (int i = 0; i < NV; ++i) {
+      const int j = i * TPR + t;
+      v[i] = (active && j < C4) ? ld4<NT>(x4 + j) : f32x4{fill, fill, fill, fill};
     }
-  }
+  };
 
   // Row reduction: wave-level, then (when the row spans wavefronts) an LDS fold in wave order.
   auto row_reduce_sum = [&](float s, float* slots) -> float {
@@ -91,65 +112,80 @@ __global__ void __launch_bounds__(TPR < 256 ? 256 : TPR)
     }
   };
 
-  if constexpr (OP == 0) {  // row-sum
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < NV; ++i) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
-    s = row_reduce_sum(s, red0);
-    if (active && t == 0) Y[row] = s;
-  } else if constexpr (OP == 1) {  // RMSNorm
+  f32x4 va[NV], vb[NV];
+  load_row(va, 0);
+  f32x4 g[NV];  // RMSNorm gain, read once per workgroup
+  if constexpr (OP == 1) {
     const f32x4* w4 = reinterpret_cast<const f32x4*>(Wg);
-    f32x4 g[NV];
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int j = i * TPR + t;
       g[i] = (j < C4) ? w4[j] : f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    float ss = 0.f;
+  }
+
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      // __fmul_rn keeps the squares unfused from the adds, as in the reference CPU loop.
-      ss += (__fmul_rn(v[i].x, v[i].x) + __fmul_rn(v[i].y, v[i].y)) +
-            (__fmul_rn(v[i].z, v[i].z) + __fmul_rn(v[i].w, v[i].w));
-    }
-    ss = row_reduce_sum(ss, red0);
-    const float rms = 1.0f / sqrtf(ss / (float)C + eps);
-    if (active) {
-      f32x4* y4 = reinterpret_cast<f32x4*>(Y + row * (int64_t)C);
+  for (int k = 0; k < RPB; ++k) {
+    f32x4(&v)[NV] = (k & 1) ? vb : va;
+    if (k + 1 < RPB) load_row((k & 1) ? va : vb, k + 1);
+    const int64_t row = row_of(k);
+    const bool active = row < L;
+    f32x4* y4 = reinterpret_cast<f32x4*>(Y + (active ? row : 0) * (int64_t)C);
+
+    if constexpr (OP == 0) {  // row-sum
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+      s = row_reduce_sum(s, red0[k & 1]);
+      if (active && t == 0) Y[row] = s;
+    } else if constexpr (OP == 1) {  // RMSNorm
+      float ss = 0.f;
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
-        const int j = i * TPR + t;
-        if (j < C4) {
-          f32x4 o;
-          o.x = __fmul_rn(__fmul_rn(v[i].x, rms), g[i].x);
-          o.y = __fmul_rn(__fmul_rn(v[i].y, rms), g[i].y);
-          o.z = __fmul_rn(__fmul_rn(v[i].z, rms), g[i].z);
-          o.w = __fmul_rn(__fmul_rn(v[i].w, rms), g[i].w);
-          st4<NT>(y4 + j, o);
+        // The compiler may contract a square with the following add (one rounding fewer).
+        ss += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
+      }
+      ss = row_reduce_sum(ss, red0[k & 1]);
+      // Correctly rounded divide and square root, as the reference's 1.0f / std::sqrt(...).
+      const float rms = 1.0f / sqrtf(ss / (float)C + eps);
+      if (active) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          const int j = i * TPR + t;
+          if (j < C4) {
+            f32x4 o;
+            o.x = (v[i].x * rms) * g[i].x;
+            o.y = (v[i].y * rms) * g[i].y;
+            o.z = (v[i].z * rms) * g[i].z;
+            o.w = (v[i].w * rms) * g[i].w;
+            st4<NT>(y4 + j, o);
+          }
         }
       }
-    }
-  } else {  // softmax
-    float m = -INFINITY;
+    } else {  // softmax
+      float m = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) m = fmaxf(m, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
-    m = row_reduce_max(m, red0);
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      v[i].x = expf(v[i].x - m);
-      v[i].y = expf(v[i].y - m);
-      v[i].z = expf(v[i].z - m);
-      v[i].w = expf(v[i].w - m);
-      s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
-    }
-    s = row_reduce_sum(s, red1);
-    if (active) {
-      f32x4* y4 = reinterpret_cast<f32x4*>(Y + row * (int64_t)C);
+      for (int i = 0; i < NV; ++i) m = fmaxf(m, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
+      m = row_reduce_max(m, red0[k & 1]);
+      float s = 0.f;
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
-        const int j = i * TPR + t;
-        if (j < C4) st4<NT>(y4 + j, f32x4{v[i].x / s, v[i].y / s, v[i].z / s, v[i].w / s});
+        v[i].x = exp_softmax(v[i].x - m);
+        v[i].y = exp_softmax(v[i].y - m);
+        v[i].z = exp_softmax(v[i].z - m);
+        v[i].w = exp_softmax(v[i].w - m);
+        s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+      }
+      s = row_reduce_sum(s, red1[k & 1]);
+      // One correctly rounded reciprocal per row, then a multiply per element: within one
+      // rounding of the reference's per-element divide.
+      const float inv = 1.0f / s;
+      if (active) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          const int j = i * TPR + t;
+          if (j < C4) st4<NT>(y4 + j, f32x4{v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv});
+        }
       }
     }
   }
@@ -271,23 +307,23 @@ __global__ void __launch_bounds__(kReduceThreads)
 namespace uk {
 
 namespace {
-template <int TPR, int NV, bool NT>
+template <int TPR, int NV, bool NT, int RPB>
 hipError_t rows_dispatch_op(RowOp op, const float* X, const float* W, float* Y, int64_t L, int64_t C, float eps,
                             hipStream_t s) {
   constexpr int WG = TPR < 256 ? 256 : TPR;
   constexpr int RPW = WG / TPR;
-  const int64_t grid = (L + RPW - 1) / RPW;
+  const int64_t grid = (L + RPW * RPB - 1) / (RPW * RPB);
   switch (op) {
     case RowOp::Sum:
-      hipLaunchKernelGGL((kern::rows_kernel<TPR, NV, 0, NT>), dim3((unsigned)grid), dim3(WG), 0, s, X, W, Y, (int)L,
+      hipLaunchKernelGGL((kern::rows_kernel<TPR, NV, 0, NT, RPB>), dim3((unsigned)grid), dim3(WG), 0, s, X, W, Y, (int)L,
                          (int)C, eps);
       break;
     case RowOp::RmsNorm:
-      hipLaunchKernelGGL((kern::rows_kernel<TPR, NV, 1, NT>), dim3((unsigned)grid), dim3(WG), 0, s, X, W, Y, (int)L,
+      hipLaunchKernelGGL((kern::rows_kernel<TPR, NV, 1, NT, RPB>), dim3((unsigned)grid), dim3(WG), 0, s, X, W, Y, (int)L,
                          (int)C, eps);
       break;
     case RowOp::Softmax:
-      hipLaunchKernelGGL((kern::rows_kernel<TPR, NV, 2, NT>), dim3((unsigned)grid), dim3(WG), 0, s, X, W, Y, (int)L,
+      hipLaunchKernelGGL((kern::rows_kernel<TPR, NV, 2, NT, RPB>), dim3((unsigned)grid), dim3(WG), 0, s, X, W, Y, (int)L,
                          (int)C, eps);
       break;
   }
@@ -324,10 +360,11 @@ hipError_t launch_rows(const Plan& p, RowOp op, const float* X, const float* W, 
   if ((C & 3) != 0 || C > (int64_t)v.tpr * v.nv * 4) return hipErrorInvalidValue;
   if ((((uintptr_t)X) & 15) || (((uintptr_t)Y) & 15) || (W && (((uintptr_t)W) & 15))) return hipErrorInvalidValue;
   switch (p.variant) {
-  static_assert(kNumRowsVariants == 21, "every rows variant needs a case below");
-#define UK_ROWS_CASE(I)                                                                                 \
-  case I:                                                                                               \
-    return rows_dispatch_op<kRowsVariants[I].tpr, kRowsVariants[I].nv, kRowsVariants[I].nt != 0>(op, X, W, Y, L, C, eps, s);
+  static_assert(kNumRowsVariants == 24, "every rows variant needs a case below");
+#define UK_ROWS_CASE(I)                                                                                   \
+  case I:                                                                                                 \
+    return rows_dispatch_op<kRowsVariants[I].tpr, kRowsVariants[I].nv, kRowsVariants[I].nt != 0,         \
+                            kRowsVariants[I].rpb>(op, X, W, Y, L, C, eps, s);
     UK_ROWS_CASE(0)
     UK_ROWS_CASE(1)
     UK_ROWS_CASE(2)
@@ -349,6 +386,9 @@ hipError_t launch_rows(const Plan& p, RowOp op, const float* X, const float* W, 
     UK_ROWS_CASE(18)
     UK_ROWS_CASE(19)
     UK_ROWS_CASE(20)
+    UK_ROWS_CASE(21)
+    UK_ROWS_CASE(22)
+    UK_ROWS_CASE(23)
 #undef UK_ROWS_CASE
     default: return hipErrorInvalidValue;
   }

@@ -9,14 +9,39 @@ namespace uk {
 // tpr: threads per row (whole wavefronts), nv: float4 registers per thread.
 // A workgroup is max(tpr, 256) threads, i.e. 256/tpr rows per workgroup when tpr < 256.
 // nt: loads and stores carry the non-temporal hint (streamed data bypasses cache retention).
+// rpb: rows a workgroup walks in turn, the next row's loads in flight during this row's reduction.
+// eff: calibrated fraction of the HBM peak the variant sustains for row-sum, RMSNorm and softmax
+// (kernel-only median at 4096 x 4096 f32 on one MI355X, rotating buffers > 512 MiB); 0 where the
+// variant cannot hold a 4096-wide row, and the solver's bytes-in-flight model prices it alone.
 struct RowsVariant {
-  int tpr, nv, nt;
+  int tpr, nv, nt, rpb;
+  double eff_sum, eff_rms, eff_softmax;
 };
 constexpr RowsVariant kRowsVariants[] = {
-    {64, 1, 0},   {64, 2, 0},   {64, 4, 0},  {64, 8, 0},    {64, 16, 0},   {128, 4, 0},
-    {128, 8, 0},  {256, 1, 0},  {256, 2, 0}, {256, 4, 0},   {256, 8, 0},   {512, 2, 0},
-    {512, 4, 0},  {1024, 1, 0}, {1024, 2, 0}, {1024, 4, 0}, {256, 4, 1},   {512, 2, 1},
-    {1024, 1, 1}, {512, 4, 1},  {1024, 2, 1},
+    {64, 1, 0, 1, 0, 0, 0},
+    {64, 2, 0, 1, 0, 0, 0},
+    {64, 4, 0, 1, 0, 0, 0},
+    {64, 8, 0, 1, 0, 0, 0},
+    {64, 16, 0, 1, 0.653, 0.622, 0.625},
+    {128, 4, 0, 1, 0, 0, 0},
+    {128, 8, 0, 1, 0.697, 0.658, 0.661},
+    {256, 1, 0, 1, 0, 0, 0},
+    {256, 2, 0, 1, 0, 0, 0},
+    {256, 4, 0, 1, 0.707, 0.679, 0.690},
+    {256, 8, 0, 1, 0.706, 0.683, 0.681},
+    {512, 2, 0, 1, 0.715, 0.694, 0.698},
+    {512, 4, 0, 1, 0.715, 0.690, 0.684},
+    {1024, 1, 0, 1, 0.549, 0.585, 0.672},
+    {1024, 2, 0, 1, 0.552, 0.583, 0.639},
+    {1024, 4, 0, 1, 0.544, 0.597, 0.526},
+    {256, 4, 1, 1, 0.754, 0.696, 0.718},
+    {512, 2, 1, 1, 0.762, 0.704, 0.735},
+    {1024, 1, 1, 1, 0.558, 0.598, 0.683},
+    {512, 4, 1, 1, 0.759, 0.702, 0.717},
+    {1024, 2, 1, 1, 0.562, 0.606, 0.642},
+    {128, 8, 1, 1, 0.740, 0.704, 0.709},
+    {256, 4, 1, 2, 0.731, 0.714, 0.698},
+    {512, 2, 1, 2, 0.742, 0.700, 0.681},
 };
 constexpr int kNumRowsVariants = sizeof(kRowsVariants) / sizeof(kRowsVariants[0]);
 constexpr int kRowsStreamThreads = 256;
