@@ -135,7 +135,7 @@ def _feasible_rows_keys(d):
 
 
 def test_calibrated_gemm_pick(uk):
-    # the variant measured fastest at 4096^3 (eight wavefronts, row>>2 swizzle) is the pick
+    # the variant measured fastest at 4096^3 (eight ping-pong wavefronts, four ring stages) is the pick
     s = uk.solve(uk.make_desc("gemm", [4096, 4096, 4096], dtype="fp16", layout="TN"))
-    assert s.key == "gemm_f16:256x256x32,w2x4,s4,z2"
+    assert s.key == "gemm_f16:256x256x32,w2x4,s4,z2,pp"
     assert s.plan.tile_m == 256 and s.plan.threads == 512

@@ -1,7 +1,7 @@
 // GEMM on gfx950 matrix cores.
 //
 // Replaces the reference's SIMT uk_gemm / uk_gemm_h (src/codegen_hip.cpp:1089-1120,
-// :1777-1808), which convert to f32 in LDS and run scalar FMAs. Two kernels:
+// :1777-1808), which convert to f32 in LDS and run scalar FMAs. Three kernels:
 //
 // gemm_f16_tn_kernel — the hot path: C[M][N] f16 = A[M][K] f16 . B^T, B stored [N][K]
 //   (column-major B: both operands K-contiguous), f32 accumulate in v_mfma_f32_32x32x16_f16.
@@ -24,6 +24,16 @@
 //   * the MFMA computes C^T tiles (B fragment as the first operand), so each lane holds four
 //     consecutive output columns per row; the epilogue converts to f16 (round to nearest
 //     even), stages the tile in LDS and writes rows with 128-bit stores.
+//
+// gemm_f16_pp_kernel — the same 256x256 tile and LDS ring, scheduled as "ping-pong": the eight
+//   wavefronts form two groups of four, one wavefront of each group per SIMD. While one group
+//   issues MFMAs (v_mfma_f32_16x16x32_f16, a k-tile's worth from registers) the other reads its
+//   next fragments from LDS and issues its share of the DMA copies; the groups swap at every
+//   workgroup barrier. A wavefront issuing LDS reads or DMA copies stalls its own MFMA stream
+//   (about 16 and 40-60 cycles per instruction, measured), so separating the roles keeps each
+//   SIMD's matrix pipe fed by a wavefront that issues nothing else. The 16x16x32 form moves half
+//   the accumulator bytes per flop of the 32x32x16 form; this chip runs the GEMM at its power
+//   limit, so the saving shows up as a higher sustained clock.
 //
 // gemm_generic_kernel — any M, N, K, either B layout, f16 or f32 inputs: 64x64 tiles,
 //   bounds-checked element loads, MFMA 32x32x16 f16 or 32x32x2 f32. Used for shapes the
@@ -267,6 +277,175 @@ __global__ void __launch_bounds__(WM* WN * 64, 1)
 }
 
 // ---------------------------------------------------------------------------------------
+// Ping-pong f16 GEMM: 256x256x32 macro tile, 8 wavefronts in two groups (g = wave / 4), wave
+// tile 128 x 64 (rows g*128.., columns (wave % 4)*64..), STAGES-deep LDS ring of k-tiles.
+//
+// Phases p = 0, 1, 2, ... are separated by workgroup barriers b_p. Group 0 reads k-tile t's
+// fragments in phase 2t and multiplies them in phase 2t+1; group 1 does the same one phase later
+// (2t+1, 2t+2). In its read phase of tile t a wavefront also issues its quarter of one operand's
+// copies of tile t + STAGES - 1 (group 0 copies A, group 1 copies B) into the slot tile t - 1
+// left: its last reader, group 1, finished with it before b_2t. Before b_{2t+2} every wavefront
+// waits until its own copies of tile t + 1 have landed, so after that barrier tile t + 1 is
+// visible to all. Both groups execute the same number of barriers (2 KT after the prologue's).
+// ---------------------------------------------------------------------------------------
+constexpr int kPpBM = 256, kPpBN = 256, kPpBK = 32;
+constexpr int kPpRow = kPpBK * 2;             // 64-byte LDS rows (4 chunks of 16 bytes)
+constexpr int kPpOp = 256 * kPpRow;           // 16 KiB per operand per stage
+constexpr int kPpStage = 2 * kPpOp;
+constexpr int kPpWTM = 128, kPpWTN = 64;
+constexpr int kPpPitch = kPpWTN * 2 + 16;     // epilogue staging row pitch (bytes)
+constexpr int kPpEpi = 8 * kPpWTM * kPpPitch;
+template <int STAGES>
+constexpr int pp_lds_bytes() { return STAGES * kPpStage > kPpEpi ? STAGES * kPpStage : kPpEpi; }
+
+// Workgroup barrier without the memory fence __syncthreads() implies: the fence would make every
+// barrier wait for all outstanding copies, and each wait this kernel needs is issued explicitly.
+__device__ __forceinline__ void barrier_nofence() { __asm__ volatile("s_barrier" ::: "memory"); }
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4)); }
+
+// Wait until at most 4 * n copies of this wavefront are outstanding (n = 0..3).
+__device__ __forceinline__ void wait_copies(int n) {
+  if (n >= 3) wait_vmcnt<12>();
+  else if (n == 2) wait_vmcnt<8>();
+  else if (n == 1) wait_vmcnt<4>();
+  else wait_vmcnt<0>();
+}
+
+template <int STAGES>
+__global__ void __launch_bounds__(512, 1)
+    gemm_f16_pp_kernel(const _Float16* __restrict__ A, const _Float16* __restrict__ B, _Float16* __restrict__ C,
+                       int M, int N, int K, int tiles_m, int tiles_n) {
+  static_assert(STAGES >= 2 && STAGES - 2 <= 3, "copies in flight must fit wait_copies");
+  typedef float f32x4v __attribute__((ext_vector_type(4)));
+  __shared__ __attribute__((aligned(1024))) char lds[pp_lds_bytes<STAGES>()];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = w >> 2, q = w & 3;
+
+  // XCD-aware tile order, as in gemm_f16_tn_kernel.
+  const int G = gridDim.x;
+  int lin = blockIdx.x;
+  if ((G & 7) == 0) lin = (lin & 7) * (G >> 3) + (lin >> 3);
+  constexpr int kGroupM = 4;
+  const int per_group = kGroupM * tiles_n;
+  const int group = lin / per_group;
+  const int first_m = group * kGroupM;
+  const int gm = (tiles_m - first_m) < kGroupM ? (tiles_m - first_m) : kGroupM;
+  const int in_group = lin - group * per_group;
+  const int tm = first_m + in_group % gm;
+  const int tn = in_group / gm;
+  const int m0 = tm * kPpBM, n0 = tn * kPpBN;
+
+  // Copies: operand g's row block; instruction ins = 4u + q (u < 4) moves rows ins*16 .. +16.
+  // Lane l fills row l / 4, physical chunk l % 4 with logical chunk (l % 4) ^ ((row >> 2) & 3);
+  // (row >> 2) & 3 = (l >> 4) & 3 for every instruction, so one lane offset serves all four.
+  const _Float16* op = g == 0 ? A + (int64_t)m0 * K : B + (int64_t)n0 * K;
+  const int vrow = lane >> 2;
+  const int voff = (vrow * K + (((lane & 3) ^ ((lane >> 4) & 3)) * 8)) * 2;
+  const int KT = K / kPpBK;
+  auto issue = [&](int t) {
+    char* st = lds + (t % STAGES) * kPpStage + g * kPpOp;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int ins = u * 4 + q;
+      copy_to_lds(op, 256 * K * 2, st + ins * 1024, voff, (ins * 16 * K + t * kPpBK) * 2);
+    }
+  };
+
+  // v_mfma_f32_16x16x32_f16 fragments: lane l supplies row l & 15 of a 16-row group at k-group
+  // (logical chunk) l >> 4; one fragment per 16-row group covers the whole k-tile.
+  const int frow = lane & 15, fk = lane >> 4;
+  f16x8 fa[8], fb[4];
+  auto read_frags = [&](int t) {
+    const char* As = lds + (t % STAGES) * kPpStage;
+    const char* Bs = As + kPpOp;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = g * kPpWTM + i * 16 + frow;
+      fa[i] = *reinterpret_cast<const f16x8*>(As + r * kPpRow + ((fk ^ ((r >> 2) & 3)) << 4));
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = q * kPpWTN + j * 16 + frow;
+      fb[j] = *reinterpret_cast<const f16x8*>(Bs + r * kPpRow + ((fk ^ ((r >> 2) & 3)) << 4));
+    }
+  };
+  // acc[i][j] = C^T block: lane l holds C[i*16 + (l & 15)][j*16 + 4*(l >> 4) + r], r < 4.
+  f32x4v acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4v{0.f, 0.f, 0.f, 0.f};
+  auto multiply = [&]() {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fb[j], fa[i], acc[i][j], 0, 0, 0);
+  };
+  // Copies of tiles issued after tile t+1 by this wavefront (they may stay in flight).
+  auto after = [&](int t) {
+    const int last = (t + STAGES - 1 < KT - 1) ? t + STAGES - 1 : KT - 1;
+    return last - (t + 1);
+  };
+
+  // Prologue: tiles 0 .. STAGES-2 (those that exist), then wait for tile 0.
+  for (int t = 0; t < STAGES - 1; ++t)
+    if (t < KT) issue(t);
+  wait_copies((STAGES - 2 < KT - 1) ? STAGES - 2 : KT - 1);
+  barrier_nofence();  // b0
+
+  if (g == 0) {
+    for (int t = 0; t < KT; ++t) {
+      read_frags(t);  // phase 2t
+      if (t + STAGES - 1 < KT) issue(t + STAGES - 1);
+      wait_lgkm0();
+      barrier_nofence();  // b_{2t+1}
+      multiply();  // phase 2t+1
+      wait_copies(after(t));
+      barrier_nofence();  // b_{2t+2}
+    }
+  } else {
+    barrier_nofence();  // b1 (phase 0: nothing to multiply yet)
+    for (int t = 0; t < KT; ++t) {
+      read_frags(t);  // phase 2t+1
+      if (t + STAGES - 1 < KT) issue(t + STAGES - 1);
+      wait_lgkm0();
+      wait_copies(after(t));
+      barrier_nofence();  // b_{2t+2}
+      multiply();  // phase 2t+2
+      if (t < KT - 1) barrier_nofence();  // b_{2t+3}
+    }
+  }
+  // After b_{2KT} no wavefront reads the ring and no copy is in flight (every wavefront waited
+  // for all of its copies before that barrier): each wavefront stages its tile in its own region.
+  char* stage = lds + w * (kPpWTM * kPpPitch);
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      f16x4 h;
+      h[0] = (_Float16)acc[i][j][0];
+      h[1] = (_Float16)acc[i][j][1];
+      h[2] = (_Float16)acc[i][j][2];
+      h[3] = (_Float16)acc[i][j][3];
+      const int m = i * 16 + (lane & 15);
+      const int n = j * 16 + 4 * (lane >> 4);
+      *reinterpret_cast<f16x4*>(stage + m * kPpPitch + n * 2) = h;
+    }
+  // The region is private to this wavefront: its own LDS writes must land before its reads.
+  __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  constexpr int kRowChunks = kPpWTN * 2 / 16;
+  _Float16* Cw = C + (int64_t)(m0 + g * kPpWTM) * N + n0 + q * kPpWTN;
+#pragma unroll 4
+  for (int id = lane; id < kPpWTM * kRowChunks; id += 64) {
+    const int r = id / kRowChunks, c = id % kRowChunks;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(stage + r * kPpPitch + c * 16);
+    *reinterpret_cast<u32x4*>(Cw + (int64_t)r * N + c * 8) = v;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // Generic MFMA GEMM: 64x64 tile, 4 wavefronts (2x2 of 32x32), BK = 16, bounds-checked.
 // T = _Float16 or float inputs; TO = output type; BT: B stored [N][K] (TN) else [K][N] (NT).
 // ---------------------------------------------------------------------------------------
@@ -328,6 +507,15 @@ namespace {
 template <int I>
 hipError_t gemm_f16_variant(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, hipStream_t s) {
   constexpr GemmF16Variant v = kGemmF16Variants[I];
+  if constexpr (v.pp) {
+    static_assert(v.bm == kern::kPpBM && v.bn == kern::kPpBN && v.bk == kern::kPpBK && v.wm * v.wn == 8,
+                  "ping-pong variants are 256x256x32 with 8 wavefronts");
+    const int tiles_m = int(M / v.bm), tiles_n = int(N / v.bn);
+    hipLaunchKernelGGL((kern::gemm_f16_pp_kernel<v.stages>), dim3((unsigned)(tiles_m * tiles_n)), dim3(512), 0, s,
+                       static_cast<const _Float16*>(A), static_cast<const _Float16*>(B), static_cast<_Float16*>(C),
+                       (int)M, (int)N, (int)K, tiles_m, tiles_n);
+    return hipGetLastError();
+  }
   using Cfg = kern::GemmF16Cfg<v.bm, v.bn, v.bk, v.wm, v.wn, v.stages>;
   const int tiles_m = int(M / v.bm), tiles_n = int(N / v.bn);
   hipLaunchKernelGGL((kern::gemm_f16_tn_kernel<v.bm, v.bn, v.bk, v.wm, v.wn, v.stages, v.swz>),
@@ -350,7 +538,7 @@ hipError_t launch_gemm_f16(const Plan& p, const void* A, const void* B, void* C,
   if (int64_t(v.bm > v.bn ? v.bm : v.bn) * K * 2 > INT32_MAX) return hipErrorInvalidValue;
   if ((((uintptr_t)A) | ((uintptr_t)B) | ((uintptr_t)C)) & 15) return hipErrorInvalidValue;
   if ((M / v.bm) * (N / v.bn) > INT32_MAX) return hipErrorInvalidValue;
-  static_assert(kNumGemmF16Variants == 10, "every GEMM variant needs a case below");
+  static_assert(kNumGemmF16Variants == 12, "every GEMM variant needs a case below");
   switch (p.variant) {
 #define UK_GEMM_CASE(I) \
   case I:                 \
@@ -365,6 +553,8 @@ hipError_t launch_gemm_f16(const Plan& p, const void* A, const void* B, void* C,
     UK_GEMM_CASE(7)
     UK_GEMM_CASE(8)
     UK_GEMM_CASE(9)
+    UK_GEMM_CASE(10)
+    UK_GEMM_CASE(11)
 #undef UK_GEMM_CASE
     default: return hipErrorInvalidValue;
   }

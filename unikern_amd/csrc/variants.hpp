@@ -50,27 +50,32 @@ constexpr int kRowsStreamThreads = 256;
 constexpr int kReduceParts = 2048;
 constexpr int kReduceThreads = 256;
 
-// f16 MFMA GEMM, layout TN (A[M][K], B stored [N][K]), v_mfma_f32_32x32x16_f16.
+// f16 MFMA GEMM, layout TN (A[M][K], B stored [N][K]).
 // bm x bn x bk macro tile; wm x wn waves; stages of LDS buffering; swz selects the LDS
-// XOR swizzle (0: row, 1: row >> 1, 2: row >> 2) for the bank geometry. eff is the calibrated
-// fraction of the dense f16 MFMA peak the variant sustains when every CU holds a tile (kernel-only
-// median at M = N = K = 4096 on one MI355X); the solver's cost model scales it by wave
-// quantisation for other shapes.
+// XOR swizzle (0: row, 1: row >> 1, 2: row >> 2) for the bank geometry. pp = 0: every wavefront
+// interleaves copies, fragment reads and v_mfma_f32_32x32x16_f16 (gemm_f16_tn_kernel); pp = 1:
+// ping-pong wavefront groups on v_mfma_f32_16x16x32_f16 (gemm_f16_pp_kernel, 256x256x32 with 8
+// wavefronts and swizzle row >> 2 only). eff is the calibrated fraction of the dense f16 MFMA peak
+// the variant sustains when every CU holds a tile (kernel-only median at M = N = K = 4096 on one
+// MI355X, clocks settled); the solver's cost model scales it by wave quantisation for other shapes.
 struct GemmF16Variant {
   int bm, bn, bk, wm, wn, stages, swz;
   double eff;
+  int pp;
 };
 constexpr GemmF16Variant kGemmF16Variants[] = {
-    {256, 256, 32, 2, 2, 4, 1, 0.371},
-    {256, 256, 32, 2, 2, 4, 2, 0.389},
-    {256, 256, 32, 2, 2, 4, 0, 0.402},
-    {256, 256, 32, 2, 4, 4, 2, 0.409},
-    {256, 128, 32, 2, 2, 4, 2, 0.326},
-    {256, 128, 64, 2, 2, 3, 1, 0.316},
-    {128, 128, 64, 2, 2, 3, 1, 0.229},
-    {128, 128, 32, 2, 2, 4, 2, 0.280},
-    {256, 256, 32, 2, 4, 5, 2, 0.408},
-    {256, 256, 32, 2, 2, 5, 2, 0.399},
+    {256, 256, 32, 2, 2, 4, 1, 0.431, 0},
+    {256, 256, 32, 2, 2, 4, 2, 0.436, 0},
+    {256, 256, 32, 2, 2, 4, 0, 0.432, 0},
+    {256, 256, 32, 2, 4, 4, 2, 0.446, 0},
+    {256, 128, 32, 2, 2, 4, 2, 0.354, 0},
+    {256, 128, 64, 2, 2, 3, 1, 0.336, 0},
+    {128, 128, 64, 2, 2, 3, 1, 0.231, 0},
+    {128, 128, 32, 2, 2, 4, 2, 0.314, 0},
+    {256, 256, 32, 2, 4, 5, 2, 0.445, 0},
+    {256, 256, 32, 2, 2, 5, 2, 0.425, 0},
+    {256, 256, 32, 2, 4, 4, 2, 0.479, 1},
+    {256, 256, 32, 2, 4, 5, 2, 0.475, 1},
 };
 constexpr int kNumGemmF16Variants = sizeof(kGemmF16Variants) / sizeof(kGemmF16Variants[0]);
 
