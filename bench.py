@@ -74,6 +74,8 @@ def _settle(uk, d, plan, in_sets, n_in, out_sets, stream):
     a 4096^3 GEMM timed right after an idle gap runs 10-15% slower for its first ~2 ms, and the
     row kernels 2-4% slower. Settling first makes every timed segment a steady-state figure,
     which is what a serving loop sees. Nothing here is timed or counted."""
+    if SETTLE_MS <= 0:
+        return
     e0, e1 = _events(uk)
     uk._check(uk.lib.uk_event_record(e0, stream))
     _launch_n(uk, d, plan, in_sets, n_in, out_sets, 5, stream)
@@ -132,26 +134,27 @@ def bench_rows(uk, O, steps: int, warmup: int, stream):
             verified[name] = mr <= 1e-5
     stats = {}
     e0, e1 = _events(uk)
-    uk._check(uk.lib.uk_synchronize())
-    t0 = time.perf_counter()
     total_ms = 0.0
+    wall = 0.0  # host clock around the timed segments only (settling and warm-up excluded)
     for name, (d, ins, n_in, outs, nbytes) in ops.items():
         sol = uk.solve(d)
         flat = [p for s in ins for p in s]
         _settle(uk, d, sol.plan, flat, n_in, outs, stream)
         if warmup:
             _launch_n(uk, d, sol.plan, flat, n_in, outs, warmup, stream)
+        uk._check(uk.lib.uk_synchronize())
+        t0 = time.perf_counter()
         uk._check(uk.lib.uk_event_record(e0, stream))
         _launch_n(uk, d, sol.plan, flat, n_in, outs, steps, stream)
         uk._check(uk.lib.uk_event_record(e1, stream))
         uk._check(uk.lib.uk_stream_synchronize(stream))
+        wall += (time.perf_counter() - t0) * 1e3
         ms = _elapsed(uk, e0, e1) / steps
         total_ms += ms
         gbs = nbytes / (ms * 1e-3) / 1e9
         stats[name] = {"ms": round(ms, 6), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
                        "bytes": nbytes, "plan": sol.key}
     uk._check(uk.lib.uk_synchronize())
-    wall = (time.perf_counter() - t0) * 1e3
     for e in (e0, e1):
         uk.lib.uk_event_destroy(e)
     step_bytes = sum(v[4] for v in ops.values())
@@ -193,7 +196,61 @@ def _time_op(uk, d, host_inputs, out_bytes, steps, warmup, stream, min_set_bytes
     return ms, sol.key, first_out, sets
 
 
-def bench_gemm(uk, O, steps: int, warmup: int, stream):
+def vendor_gemm(A, B, steps: int, warmup: int, sets: int):
+    """The same f16 GEMM through the vendor library (torch.mm -> hipBLASLt) on the same inputs,
+    in a child process: torch ships its own HIP runtime, which does not share a process with the
+    one this library links. Context for the roofline fraction only; nothing of the product runs
+    through it."""
+    import subprocess
+    import tempfile
+
+    with tempfile.TemporaryDirectory() as td:
+        np.save(Path(td) / "a.npy", A)
+        np.save(Path(td) / "b.npy", B)
+        p = subprocess.run([sys.executable, str(Path(__file__).resolve()), "--vendor-child", td, "--steps", str(steps),
+                            "--warmup", str(warmup), "--settle-ms", str(SETTLE_MS), "--sets", str(sets)],
+                           capture_output=True, text=True, timeout=600)
+        if p.returncode != 0:
+            raise RuntimeError(f"vendor GEMM child failed: {p.stderr[-2000:]}")
+        res = json.loads(p.stdout.strip().splitlines()[-1])
+    return res["ms"], np.array(res["row0"], dtype=np.float32)[None, :]
+
+
+def _vendor_child(td: str, steps: int, warmup: int, sets: int) -> None:
+    import torch
+
+    A = np.load(Path(td) / "a.npy")
+    B = np.load(Path(td) / "b.npy")
+    M, K = A.shape
+    N = B.shape[0]
+    a = [torch.from_numpy(A.view(np.float16)).cuda() for _ in range(sets)]
+    b = [torch.from_numpy(B.view(np.float16)).cuda() for _ in range(sets)]
+    c = [torch.empty(M, N, device="cuda", dtype=torch.float16) for _ in range(sets)]
+
+    def run(n):
+        for i in range(n):
+            torch.mm(a[i % sets], b[i % sets].t(), out=c[i % sets])
+
+    run(1)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    run(5)
+    e1.record()
+    torch.cuda.synchronize()
+    if SETTLE_MS > 0:
+        run(int(min(20000, SETTLE_MS / max(e0.elapsed_time(e1) / 5, 1e-3))))
+    run(warmup)
+    e0.record()
+    run(steps)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    row0 = c[(steps - 1) % sets][0].float().cpu().numpy()
+    print(json.dumps({"ms": ms, "row0": row0.tolist()}), flush=True)
+
+
+def bench_gemm(uk, O, steps: int, warmup: int, stream, vendor: bool = False):
     M = N = K = 4096
     A = O.f16_bits(O.uniform(M * K, SEED + 20, -1.0, 1.0)).reshape(M, K)
     B = O.f16_bits(O.uniform(N * K, SEED + 21, -1.0, 1.0)).reshape(N, K)
@@ -205,10 +262,16 @@ def bench_gemm(uk, O, steps: int, warmup: int, stream):
     R = O.gemm_f16q(A[rows], B, True).astype(np.float64)
     fro = float(np.linalg.norm(Cg - R) / np.linalg.norm(R))
     tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
-    return {"workload": "gemm f16 4096^3, A row-major, B column-major, f32 accumulate, f16 out (configs[2])",
-            "ms": round(ms, 6), "value": round(tflops, 1), "unit": "TFLOP/s",
-            "frac_peak": round(tflops / F16_PEAK_TFLOPS, 4), "peak": F16_PEAK_TFLOPS, "plan": key,
-            "frobenius_rel": fro, "verified": fro <= 1e-2, "sets": sets}
+    out = {"workload": "gemm f16 4096^3, A row-major, B column-major, f32 accumulate, f16 out (configs[2])",
+           "ms": round(ms, 6), "value": round(tflops, 1), "unit": "TFLOP/s",
+           "frac_peak": round(tflops / F16_PEAK_TFLOPS, 4), "peak": F16_PEAK_TFLOPS, "plan": key,
+           "frobenius_rel": fro, "verified": fro <= 1e-2, "sets": sets}
+    if vendor:
+        vms, row0 = vendor_gemm(A, B, steps, warmup, sets)
+        vfro = float(np.linalg.norm(row0[0].astype(np.float64) - R[0]) / np.linalg.norm(R[0]))
+        out["vendor"] = {"library": "torch.mm (hipBLASLt)", "ms": round(vms, 6),
+                         "value": round(2.0 * M * N * K / (vms * 1e-3) / 1e12, 1), "frobenius_rel_row0": vfro}
+    return out
 
 
 def bench_gemm_f32(uk, O, steps: int, warmup: int, stream):
@@ -342,7 +405,18 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true", help="skip the GEMM, conv and Q8_0 configs")
+    ap.add_argument("--vendor-child", default=None, help=argparse.SUPPRESS)
+    ap.add_argument("--sets", type=int, default=7, help=argparse.SUPPRESS)
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="also time the f16 GEMM through torch.mm (hipBLASLt) on the same inputs, for context")
+    ap.add_argument("--settle-ms", type=float, default=50.0,
+                    help="untimed run of each kernel before its warm-up steps (0: none; counter passes use 0)")
     args = ap.parse_args()
+    global SETTLE_MS  # noqa: PLW0603 (set once, before any timing)
+    SETTLE_MS = args.settle_ms
+    if args.vendor_child:
+        _vendor_child(args.vendor_child, args.steps, args.warmup, args.sets)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(the kernels shard without exchange, see DESIGN.md)", file=sys.stderr)
@@ -361,7 +435,7 @@ def main():
     secondary = []
     if not args.no_secondary:
         sec_steps, sec_warm = max(10, args.steps // 2), max(5, args.warmup // 2)
-        secondary.append(bench_gemm(uk, O, sec_steps, sec_warm, stream))
+        secondary.append(bench_gemm(uk, O, sec_steps, sec_warm, stream, vendor=args.vendor_gemm))
         secondary.append(bench_gemm_f32(uk, O, sec_steps, sec_warm, stream))
         secondary.append(bench_copy(uk, O, sec_steps, sec_warm, stream))
         secondary.append(bench_conv(uk, O, sec_steps, sec_warm, stream))

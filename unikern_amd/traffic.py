@@ -22,13 +22,13 @@ from collections import defaultdict
 from pathlib import Path
 
 # Name patterns (demangled or mangled, as rocprofv3 prints them) of the kernels bench.py launches;
-# rows_kernel<TPR, NV, op> with op 0 row-sum, 1 RMSNorm, 2 softmax.
+# rows_kernel<TPR, NV, op, ...> with op 0 row-sum, 1 RMSNorm, 2 softmax.
 KERNELS = {
-    "rowsum": re.compile(r"rows_kernel<\d+, \d+, 0>|rows_kernel.*RowOpE0E"),
-    "rmsnorm": re.compile(r"rows_kernel<\d+, \d+, 1>|rows_kernel.*RowOpE1E"),
-    "softmax": re.compile(r"rows_kernel<\d+, \d+, 2>|rows_kernel.*RowOpE2E"),
+    "rowsum": re.compile(r"rows_kernel<\d+, \d+, 0[,>]"),
+    "rmsnorm": re.compile(r"rows_kernel<\d+, \d+, 1[,>]"),
+    "softmax": re.compile(r"rows_kernel<\d+, \d+, 2[,>]"),
     "copy": re.compile(r"channelscale4_kernel"),
-    "gemm_f16": re.compile(r"gemm_f16_tn_kernel"),
+    "gemm_f16": re.compile(r"gemm_f16_(tn|pp)_kernel"),
     "gemm_generic": re.compile(r"gemm_generic_kernel"),
     "conv": re.compile(r"conv_igemm_kernel|conv_tile_kernel"),
     "q8_0": re.compile(r"q8_0_gemm_kernel"),
