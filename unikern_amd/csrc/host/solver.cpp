@@ -331,11 +331,22 @@ std::optional<Plan> solve_conv(const Hcs& h, const KmlTree& t, const Shape& s, S
     const ConvVariant v = kConvVariants[i];
     std::ostringstream key;
     const bool tile = v.tile_strips > 0;
-    if (tile) key << "conv_tile:s" << v.tile_strips << ",cb" << v.bk_bytes;
+    const bool ldsk = v.tile_strips < 0;
+    if (ldsk) key << "conv_lds:64x64,cb" << v.bk_bytes;
+    else if (tile) key << "conv_tile:s" << v.tile_strips << ",cb" << v.bk_bytes;
     else key << "conv_igemm:w" << v.waves << ",lds" << v.bk_bytes;
     int64_t cb = 0, lds = 0, wgs = 0;
     double tiles_per_wave = 0;
-    if (tile) {
+    if (ldsk) {
+      if (!conv_lds_supported(t.layout == Layout::NCHW, s.Kh, s.Kw, s.stride, s.pad, s.W, s.Ho, s.Wo, s.Ci)) {
+        reject(log, key.str() + " violates NCHW 3x3 stride 1 pad<=1, W+2pad<=64, W%4==0, C%8==0, Wo>=13");
+        continue;
+      }
+      cb = v.bk_bytes;
+      lds = 2 * (2 * kConvLdsRows * kConvLdsCols * 4 + 64 * 76) * 4;
+      wgs = ((s.Ho * s.Wo + 63) / 64) * s.Nb * oc_tiles;
+      tiles_per_wave = 1;
+    } else if (tile) {
       if (taps != 9 && taps != 1) {
         reject(log, key.str() + " violates taps in {9, 1} (compiled kernel sizes)");
         continue;

@@ -378,6 +378,152 @@ __global__ void __launch_bounds__(S * 2 * 64)
   }
 }
 
+// conv_lds_kernel: NCHW, 3x3, stride 1. Both MFMA operands come from LDS: a workgroup owns 64
+// consecutive output pixels of one image (flattened Ho*Wo order) x 64 output channels, four
+// wavefronts of 32 x 32. Per chunk of 8 input channels it stages
+//   * the input rows those pixels touch, zero-padded, as xl[quad][row][col][4 channels] (the 8
+//     channels split in two quads of 4; one 16-byte entry per (quad, row, col)), and
+//   * the chunk's weights as wl[oc][tap][8 channels] (pitch 76 floats per oc: 16 lanes reading
+//     16 bytes at consecutive oc hit 16 distinct bank groups),
+// so that for each tap one ds_read_b128 of each gives a lane four k values for four
+// v_mfma_f32_32x32x2f32: MFMA j of a tap pairs channel j (lanes 0-31, k = 0) with channel 4 + j
+// (lanes 32-63, k = 1). The gathered-input kernels issue one global load per MFMA, and a load
+// costs its wavefront about as many issue cycles as the MFMA itself; here each tap's input
+// entries are read from LDS by the nine taps that share them. The next chunk's global loads are
+// in flight (in registers) while the current chunk is multiplied; one barrier per chunk.
+// Requires: 3x3 kernel, stride 1, pad 0 or 1, W + 2*pad <= kLdsCols, W and C multiples of 4 and
+// 8 (16-byte rows and whole channel chunks), 16-byte aligned X and W, and 64 consecutive output
+// pixels spanning at most kLdsRows - 2 output rows (Wo >= 13); the launcher checks.
+constexpr int kLdsRows = kConvLdsRows;
+constexpr int kLdsCols = kConvLdsCols;
+constexpr int kWPitch = 76;                                    // floats per output channel in wl
+constexpr int kXlFloats = 2 * kLdsRows * kLdsCols * 4;         // 4096 floats = 16 KiB
+constexpr int kWlFloats = 64 * kWPitch;                        // 4864 floats = 19 KiB
+constexpr int kConvLdsBuf = kXlFloats + kWlFloats;
+
+__global__ void __launch_bounds__(256)
+    conv_lds_kernel(ConvArgs a) {
+  __shared__ __attribute__((aligned(16))) float lds[2 * kConvLdsBuf];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int oh = wave & 1, ph = wave >> 1;  // output-channel half, pixel half
+  const int P = a.Ho * a.Wo;
+  const int tiles = (P + 63) / 64;
+  const int n = blockIdx.x / tiles;
+  const int p0 = (blockIdx.x - n * tiles) * 64;
+  const int r0 = p0 / a.Wo;
+  const int rlast = ((p0 + 63 < P) ? p0 + 63 : P - 1) / a.Wo;
+  const int in_rows = rlast - r0 + 3;  // padded input rows r0 .. rlast + 2
+  const int cols = a.W + 2 * a.pad;
+  const int oc_base = blockIdx.y * 64;
+  const float* xn = a.x + (int64_t)n * a.C * a.H * a.W;
+  const int64_t HW = (int64_t)a.H * a.W;
+
+  // Staging, with 16-byte global loads. Input: task (quad q, row rr, column group g) loads the
+  // four channels of the quad at input columns 4g .. 4g+3 of one row (four float4 loads along W),
+  // transposes them in registers and writes four 16-byte entries [q][rr][pad + 4g + i][0..3];
+  // the padding columns stay zero from the prologue. Weights: task (oc, channel quad h) loads the
+  // 36 contiguous floats W[oc][c0 + 4h .. +4][0..9] (nine float4) and writes one 16-byte entry
+  // wl[oc][t][4h .. 4h+3] per tap. Every thread takes input task tid mod in_tasks (at most 256
+  // tasks) and weight task tid mod 128: threads that share a task write the same values, and no
+  // staging step is under a branch, so the compiler's wait counting keeps the loads in flight
+  // across the MFMAs. Loads always use valid addresses (rows outside the image read row 0, output
+  // channels past Oc read channel 0); the zero masks apply when the registers are written to LDS.
+  const int groups = a.W / 4;
+  const int it = tid % (2 * in_rows * groups);
+  const int iq = it / (in_rows * groups);
+  const int irr = (it / groups) % in_rows, ig = it % groups;
+  const int ihi = r0 + irr - a.pad;
+  const bool in_ok = ihi >= 0 && ihi < a.H;
+  const int64_t in_off = (int64_t)4 * iq * HW + (int64_t)(in_ok ? ihi : 0) * a.W + 4 * ig;
+  float* const in_dst0 = lds + ((iq * kLdsRows + irr) * kLdsCols + a.pad + 4 * ig) * 4;
+  const int wocl = (tid & 127) >> 1, wh = tid & 1;
+  const bool w_ok = oc_base + wocl < a.Oc;
+  const float* const w_src0 = a.w + ((int64_t)(w_ok ? oc_base + wocl : 0) * a.C + 4 * wh) * 9;
+  float* const w_dst0 = lds + kXlFloats + wocl * kWPitch + 4 * wh;
+  f32x4 xs[4];
+  f32x4 ws[9];
+  auto load_chunk = [&](int c0) {
+    const float* src = xn + (int64_t)c0 * HW + in_off;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xs[j] = *reinterpret_cast<const f32x4*>(src + j * HW);
+    const float* wsrc = w_src0 + (int64_t)c0 * 9;
+#pragma unroll
+    for (int i = 0; i < 9; ++i) ws[i] = *reinterpret_cast<const f32x4*>(wsrc + 4 * i);
+  };
+  auto store_chunk = [&](int b) {
+    // Rows above or below the image are zero padding (a select: the loaded row may hold inf).
+    float* dst = in_dst0 + b * kConvLdsBuf;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<f32x4*>(dst + 4 * i) =
+          in_ok ? f32x4{xs[0][i], xs[1][i], xs[2][i], xs[3][i]} : f32x4{0.f, 0.f, 0.f, 0.f};
+    // ws holds W[oc][c0 + 4 wh + j][t] at flat index 9 j + t (j < 4, t < 9). Output channels
+    // past Oc get zero weights.
+    float* wdst = w_dst0 + b * kConvLdsBuf;
+    const float* f = reinterpret_cast<const float*>(ws);
+#pragma unroll
+    for (int t = 0; t < 9; ++t)
+      *reinterpret_cast<f32x4*>(wdst + 8 * t) =
+          w_ok ? f32x4{f[t], f[9 + t], f[18 + t], f[27 + t]} : f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+
+  // This lane's pixel (column of the MFMA tile) and k half.
+  const int pix = p0 + 32 * ph + (lane & 31);
+  const bool pvalid = pix < P;
+  const int prow = pvalid ? pix / a.Wo - r0 : 0, pcol = pvalid ? pix % a.Wo : 0;
+  const int kk = lane >> 5;
+  const int xbase = ((kk * kLdsRows + prow) * kLdsCols + pcol) * 4;  // tap (0, 0), this lane's quad
+  const int wbase = kXlFloats + (oh * 32 + (lane & 31)) * kWPitch + 4 * kk;
+
+  f32x16 acc[4] = {f32x16{}, f32x16{}, f32x16{}, f32x16{}};
+  load_chunk(0);
+  for (int i = tid; i < 2 * kXlFloats / 4; i += 256) {  // zero padding in both input buffers
+    const int b = i / (kXlFloats / 4), e = i % (kXlFloats / 4);
+    *reinterpret_cast<f32x4*>(lds + b * kConvLdsBuf + 4 * e) = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  __syncthreads();
+  store_chunk(0);
+  __syncthreads();
+  const int chunks = a.C / 8;
+  for (int k = 0; k < chunks; ++k) {
+    const float* cur = lds + (k & 1) * kConvLdsBuf;
+    // The next chunk's loads (the last chunk's again on the final pass: a cheap, unbranched
+    // repeat) are in flight while this chunk is multiplied.
+    load_chunk(8 * (k + 1 < chunks ? k + 1 : k));
+    __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the MFMAs
+#pragma unroll
+    for (int t = 0; t < 9; ++t) {
+      const int kh = t / 3, kw = t % 3;
+      const f32x4 xv = *reinterpret_cast<const f32x4*>(cur + xbase + (kh * kLdsCols + kw) * 4);
+      const f32x4 wv = *reinterpret_cast<const f32x4*>(cur + wbase + t * 8);
+      // One accumulator per channel slot j: the four MFMAs of a tap are independent.
+      acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(wv.x, xv.x, acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(wv.y, xv.y, acc[1], 0, 0, 0);
+      acc[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(wv.z, xv.z, acc[2], 0, 0, 0);
+      acc[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(wv.w, xv.w, acc[3], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // no use of the loaded registers ahead of the MFMAs
+    // The other buffer's last readers (chunk k - 1) all passed the previous barrier. The store
+    // is unconditional (after the last chunk it writes a buffer nobody reads) so that the
+    // loads above stay where they are instead of sinking into a branch behind the MFMAs.
+    store_chunk((k + 1) & 1);
+    if (k + 1 < chunks) __syncthreads();
+  }
+
+  // Epilogue: lane -> pixel (column), rows oc = oc_base + 32 oh + 8 (r / 4) + 4 kk + r % 4.
+  if (!pvalid) return;
+  float* yb = a.y + (int64_t)n * a.Oc * P;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int oc = oc_base + oh * 32 + (r >> 2) * 8 + kk * 4 + (r & 3);
+    if (oc < a.Oc) {
+      const float v = (acc[0][r] + acc[1][r]) + (acc[2][r] + acc[3][r]);
+      yb[(int64_t)oc * P + pix] = a.scale ? v * a.scale[oc] : v;
+    }
+  }
+}
+
 }  // namespace uk::kern
 
 namespace uk {
@@ -452,6 +598,15 @@ hipError_t launch_conv_igemm(const Plan& p, const Shape& sh, Layout lay, const f
   a.Ho = (int)sh.Ho;
   a.Wo = (int)sh.Wo;
   a.strips = (int)((sh.Ho * sh.Wo + 31) / 32);
+  if (v.tile_strips < 0) {  // conv_lds_kernel: NCHW 3x3 stride 1, both operands staged in LDS
+    if (!conv_lds_supported(nchw, sh.Kh, sh.Kw, sh.stride, sh.pad, sh.W, sh.Ho, sh.Wo, sh.Ci)) return hipErrorInvalidValue;
+    if ((((uintptr_t)X) | ((uintptr_t)Wt)) & 15) return hipErrorInvalidValue;
+    const int64_t tiles = (sh.Ho * sh.Wo + 63) / 64;
+    const int oc_tiles = (int)((sh.Co + 63) / 64);
+    if (sh.Nb * tiles > INT32_MAX || oc_tiles > 65535) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(kern::conv_lds_kernel, dim3((unsigned)(sh.Nb * tiles), (unsigned)oc_tiles), dim3(256), 0, s, a);
+    return hipGetLastError();
+  }
   if (v.tile_strips > 0) {  // 32 x 32 wavefront tiles, chunked coalesced weight staging
     if (taps != 9 && taps != 1) return hipErrorInvalidValue;
     a.cb = v.bk_bytes;  // channels per chunk

@@ -30,7 +30,7 @@ KERNELS = {
     "copy": re.compile(r"channelscale4_kernel"),
     "gemm_f16": re.compile(r"gemm_f16_(tn|pp)_kernel"),
     "gemm_generic": re.compile(r"gemm_generic_kernel"),
-    "conv": re.compile(r"conv_igemm_kernel|conv_tile_kernel"),
+    "conv": re.compile(r"conv_igemm_kernel|conv_tile_kernel|conv_lds_kernel"),
     "q8_0": re.compile(r"q8_0_gemm_kernel"),
 }
 COPY_BYTES_READ = 4096 * 4096 * 4 + 4096 * 4
