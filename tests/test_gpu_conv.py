@@ -83,15 +83,15 @@ def test_nchw_shapes(gpu, N, C, H, W, Oc, Kh, Kw, pad, stride):
 # Compiled conv variants (table order): 0-3 the wide kernel (any taps <= 49), 4-6 the tile
 # kernel (3x3 and 1x1 only), 7 the LDS kernel (NCHW 3x3 stride 1, pad <= 1, W + 2 pad <= 64,
 # Wo >= 13).
-CONV_VARIANTS = 8
+CONV_VARIANTS = 9
 TILE_VARIANTS = range(4, 7)
-LDS_VARIANT = 7
+LDS_VARIANTS = {7: 64, 8: 128}  # variant -> output pixels per workgroup
 
 
-def lds_supported(C, H, W, Kh, Kw, pad, stride=1, nchw=True):
+def lds_supported(C, H, W, Kh, Kw, pad, stride=1, nchw=True, pix=64):
     Wo = (W + 2 * pad - Kw) // stride + 1
     return (nchw and Kh == 3 and Kw == 3 and stride == 1 and pad in (0, 1) and W + 2 * pad <= 64
-            and W % 4 == 0 and C % 8 == 0 and (63 + Wo - 1) // Wo + 3 <= 8)
+            and W % 4 == 0 and C % 8 == 0 and (pix - 1 + Wo - 1) // Wo + 3 <= 8)
 
 
 @pytest.mark.parametrize("vi", range(CONV_VARIANTS))
@@ -103,7 +103,7 @@ def test_every_conv_variant(gpu, vi, shape):
     p = gpu.Plan()
     p.family, p.variant = 7, vi
     x, w, s = rand_conv(N, C, H, W, Oc, Kh, Kw, 100 + vi + C)
-    if vi == LDS_VARIANT and not lds_supported(C, H, W, Kh, Kw, pad):
+    if vi in LDS_VARIANTS and not lds_supported(C, H, W, Kh, Kw, pad, pix=LDS_VARIANTS[vi]):
         with pytest.raises(gpu.UnikernError):
             conv_nchw_gpu(gpu, x, w, s, pad=pad, plan=p)
         return
@@ -118,8 +118,8 @@ def test_every_conv_variant_exact_and_hwc(gpu, vi):
     x = O.sawtooth(2 * 24 * 15 * 15, 17, 8).reshape(2, 24, 15, 15)
     w = O.sawtooth(64 * 24 * 9, 13, 6).reshape(64, 24, 3, 3)
     s = O.sawtooth(64, 7, 3, bias=1.0)
-    if vi == LDS_VARIANT:  # W = 15 is not a multiple of 4; the LDS variant's exact-mode case is in test_lds_variant_shapes
-        assert not lds_supported(24, 15, 15, 3, 3, 1)
+    if vi in LDS_VARIANTS:  # W = 15 is not a multiple of 4; the LDS variants' exact-mode cases are in test_lds_variant_shapes
+        assert not lds_supported(24, 15, 15, 3, 3, 1, pix=LDS_VARIANTS[vi])
         with pytest.raises(gpu.UnikernError):
             conv_nchw_gpu(gpu, x, w, s, pad=1, plan=p)
     else:
@@ -128,7 +128,7 @@ def test_every_conv_variant_exact_and_hwc(gpu, vi):
     H, W, C, Kh, Kw, Oc = 12, 10, 6, 3, 3, 40
     xh = O.normal(H * W * C, 50 + vi, 0.0, 1.0)
     wt = O.normal(Oc * Kh * Kw * C, 60 + vi, 0.0, 0.3)
-    if vi == LDS_VARIANT:  # NCHW only: the reference's HWC layout is refused
+    if vi in LDS_VARIANTS:  # NCHW only: the reference's HWC layout is refused
         with pytest.raises(gpu.UnikernError):
             conv_hwc_gpu(gpu, xh, wt, H, W, C, Kh, Kw, Oc, plan=p)
         return
@@ -145,17 +145,24 @@ def test_tile_variants_refuse_other_kernel_sizes(gpu, vi):
         conv_nchw_gpu(gpu, x, w, s, pad=2, plan=p)
 
 
+@pytest.mark.parametrize("vi", sorted(LDS_VARIANTS))
 @pytest.mark.parametrize("N,C,H,W,Oc,pad", [
     (8, 64, 56, 56, 64, 1),   # the BASELINE shape (the solver's pick runs it in test_baseline_*)
-    (1, 16, 13, 16, 70, 1),   # Wo = 16: 64 pixels span five output rows; two oc tiles
+    (1, 16, 13, 16, 70, 1),   # Wo = 16: 64 pixels span five output rows (128 span nine: refused); two oc tiles
     (2, 8, 62, 60, 64, 1),    # W + 2 pad = 62, nearly the widest staged tile
     (1, 24, 20, 64, 3, 0),    # pad 0, W = 64 (the widest), Oc < 64, three chunks
-    (3, 16, 15, 40, 64, 1),   # plane not a multiple of 64 pixels
+    (3, 16, 15, 40, 64, 1),   # plane not a multiple of 64 (or 128) pixels
+    (2, 8, 30, 28, 40, 1),    # Wo = 28: 128 pixels span six output rows, all eight staged rows used
 ])
-def test_lds_variant_shapes(gpu, N, C, H, W, Oc, pad):
+def test_lds_variant_shapes(gpu, vi, N, C, H, W, Oc, pad):
     assert lds_supported(C, H, W, 3, 3, pad)
     p = gpu.Plan()
-    p.family, p.variant = 7, LDS_VARIANT
+    p.family, p.variant = 7, vi
+    if not lds_supported(C, H, W, 3, 3, pad, pix=LDS_VARIANTS[vi]):
+        x, w, s = rand_conv(N, C, H, W, Oc, 3, 3, 5)
+        with pytest.raises(gpu.UnikernError):
+            conv_nchw_gpu(gpu, x, w, s, pad=pad, plan=p)
+        return
     x, w, s = rand_conv(N, C, H, W, Oc, 3, 3, 200 + C + W)
     for scale in (s, None):
         y = conv_nchw_gpu(gpu, x, w, scale, pad=pad, plan=p)
@@ -166,13 +173,14 @@ def test_lds_variant_shapes(gpu, N, C, H, W, Oc, pad):
     assert np.array_equal(y.view(np.uint32), O.conv_nchw(xs, ws, None, pad=pad).view(np.uint32))
 
 
-def test_lds_variant_refuses_unsupported(gpu):
+@pytest.mark.parametrize("vi", sorted(LDS_VARIANTS))
+def test_lds_variant_refuses_unsupported(gpu, vi):
     p = gpu.Plan()
-    p.family, p.variant = 7, LDS_VARIANT
+    p.family, p.variant = 7, vi
     for (C, H, W, Oc, K, pad, stride) in [(8, 20, 20, 8, 5, 2, 1), (8, 20, 20, 8, 3, 1, 2), (8, 20, 68, 8, 3, 1, 1),
                                           (8, 20, 8, 8, 3, 1, 1), (8, 20, 20, 8, 3, 2, 1), (4, 20, 20, 8, 3, 1, 1),
                                           (8, 20, 18, 8, 3, 1, 1)]:
-        assert not lds_supported(C, H, W, K, K, pad, stride)
+        assert not lds_supported(C, H, W, K, K, pad, stride, pix=LDS_VARIANTS[vi])
         x, w, s = rand_conv(1, C, H, W, Oc, K, K, 5)
         with pytest.raises(gpu.UnikernError):
             conv_nchw_gpu(gpu, x, w, s, pad=pad, stride=stride, plan=p)

@@ -332,19 +332,21 @@ std::optional<Plan> solve_conv(const Hcs& h, const KmlTree& t, const Shape& s, S
     std::ostringstream key;
     const bool tile = v.tile_strips > 0;
     const bool ldsk = v.tile_strips < 0;
-    if (ldsk) key << "conv_lds:64x64,cb" << v.bk_bytes;
+    if (ldsk) key << "conv_lds:" << -64 * v.tile_strips << "x64,cb" << v.bk_bytes;
     else if (tile) key << "conv_tile:s" << v.tile_strips << ",cb" << v.bk_bytes;
     else key << "conv_igemm:w" << v.waves << ",lds" << v.bk_bytes;
     int64_t cb = 0, lds = 0, wgs = 0;
     double tiles_per_wave = 0;
     if (ldsk) {
-      if (!conv_lds_supported(t.layout == Layout::NCHW, s.Kh, s.Kw, s.stride, s.pad, s.W, s.Ho, s.Wo, s.Ci)) {
-        reject(log, key.str() + " violates NCHW 3x3 stride 1 pad<=1, W+2pad<=64, W%4==0, C%8==0, Wo>=13");
+      const int64_t pix = -64 * v.tile_strips;
+      if (!conv_lds_supported(t.layout == Layout::NCHW, s.Kh, s.Kw, s.stride, s.pad, s.W, s.Ho, s.Wo, s.Ci, pix)) {
+        reject(log, key.str() + " violates NCHW 3x3 stride 1 pad<=1, W+2pad<=64, W%4==0, C%8==0, " + std::to_string(pix) +
+                        " pixels within 6 output rows");
         continue;
       }
       cb = v.bk_bytes;
       lds = 2 * (2 * kConvLdsRows * kConvLdsCols * 4 + 64 * 76) * 4;
-      wgs = ((s.Ho * s.Wo + 63) / 64) * s.Nb * oc_tiles;
+      wgs = ((s.Ho * s.Wo + pix - 1) / pix) * s.Nb * oc_tiles;
       tiles_per_wave = 1;
     } else if (tile) {
       if (taps != 9 && taps != 1) {
@@ -384,7 +386,7 @@ std::optional<Plan> solve_conv(const Hcs& h, const KmlTree& t, const Shape& s, S
     c.plan.family = Family::ConvIgemm;
     c.plan.variant = i;
     c.plan.tile_m = tile ? 32 : 64;
-    c.plan.tile_n = 32 * (tile ? v.tile_strips : v.waves);
+    c.plan.tile_n = ldsk ? -64 * v.tile_strips : 32 * (tile ? v.tile_strips : v.waves);
     c.plan.tile_k = int(cb * taps);
     c.plan.threads = v.waves * 64;
     c.plan.grid = wgs;

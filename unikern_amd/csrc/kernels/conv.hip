@@ -378,9 +378,10 @@ __global__ void __launch_bounds__(S * 2 * 64)
   }
 }
 
-// conv_lds_kernel: NCHW, 3x3, stride 1. Both MFMA operands come from LDS: a workgroup owns 64
-// consecutive output pixels of one image (flattened Ho*Wo order) x 64 output channels, four
-// wavefronts of 32 x 32. Per chunk of 8 input channels it stages
+// conv_lds_kernel<PT>: NCHW, 3x3, stride 1. Both MFMA operands come from LDS: a workgroup of
+// 4 PT wavefronts owns 64 PT consecutive output pixels of one image (flattened Ho*Wo order) x 64
+// output channels, each wavefront a 32 x 32 quarter of a 64-pixel tile. Per chunk of 8 input
+// channels it stages
 //   * the input rows those pixels touch, zero-padded, as xl[quad][row][col][4 channels] (the 8
 //     channels split in two quads of 4; one 16-byte entry per (quad, row, col)), and
 //   * the chunk's weights as wl[oc][tap][8 channels] (pitch 76 floats per oc: 16 lanes reading
@@ -390,10 +391,11 @@ __global__ void __launch_bounds__(S * 2 * 64)
 // (lanes 32-63, k = 1). The gathered-input kernels issue one global load per MFMA, and a load
 // costs its wavefront about as many issue cycles as the MFMA itself; here each tap's input
 // entries are read from LDS by the nine taps that share them. The next chunk's global loads are
-// in flight (in registers) while the current chunk is multiplied; one barrier per chunk.
+// in flight (in registers) while the current chunk is multiplied; one barrier per chunk. With
+// PT = 2 the chunk's weights (the same for every pixel) are staged once per 128 pixels.
 // Requires: 3x3 kernel, stride 1, pad 0 or 1, W + 2*pad <= kLdsCols, W and C multiples of 4 and
-// 8 (16-byte rows and whole channel chunks), 16-byte aligned X and W, and 64 consecutive output
-// pixels spanning at most kLdsRows - 2 output rows (Wo >= 13); the launcher checks.
+// 8 (16-byte rows and whole channel chunks), 16-byte aligned X and W, and 64 PT consecutive
+// output pixels spanning at most kLdsRows - 2 output rows; the launcher checks.
 constexpr int kLdsRows = kConvLdsRows;
 constexpr int kLdsCols = kConvLdsCols;
 constexpr int kWPitch = 76;                                    // floats per output channel in wl
@@ -401,31 +403,30 @@ constexpr int kXlFloats = 2 * kLdsRows * kLdsCols * 4;         // 4096 floats = 
 constexpr int kWlFloats = 64 * kWPitch;                        // 4864 floats = 19 KiB
 constexpr int kConvLdsBuf = kXlFloats + kWlFloats;
 
-__global__ void __launch_bounds__(256)
+template <int PT>
+__global__ void __launch_bounds__(256 * PT)
     conv_lds_kernel(ConvArgs a) {
+  constexpr int kThreads = 256 * PT, kPix = 64 * PT;
   __shared__ __attribute__((aligned(16))) float lds[2 * kConvLdsBuf];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int oh = wave & 1, ph = wave >> 1;  // output-channel half, pixel half
+  const int oh = wave & 1, ph = wave >> 1;  // output-channel half, 32-pixel group
   const int P = a.Ho * a.Wo;
-  const int tiles = (P + 63) / 64;
+  const int tiles = (P + kPix - 1) / kPix;
   const int n = blockIdx.x / tiles;
-  const int p0 = (blockIdx.x - n * tiles) * 64;
+  const int p0 = (blockIdx.x - n * tiles) * kPix;
   const int r0 = p0 / a.Wo;
-  const int rlast = ((p0 + 63 < P) ? p0 + 63 : P - 1) / a.Wo;
+  const int rlast = ((p0 + kPix - 1 < P) ? p0 + kPix - 1 : P - 1) / a.Wo;
   const int in_rows = rlast - r0 + 3;  // padded input rows r0 .. rlast + 2
-  const int cols = a.W + 2 * a.pad;
   const int oc_base = blockIdx.y * 64;
   const float* xn = a.x + (int64_t)n * a.C * a.H * a.W;
   const int64_t HW = (int64_t)a.H * a.W;
 
-  // Staging, with 16-byte global loads. Input: task (quad q, row rr, column group g) loads the
+  // Input staging, with 16-byte global loads: task (quad q, row rr, column group g) loads the
   // four channels of the quad at input columns 4g .. 4g+3 of one row (four float4 loads along W),
   // transposes them in registers and writes four 16-byte entries [q][rr][pad + 4g + i][0..3];
-  // the padding columns stay zero from the prologue. Weights: task (oc, channel quad h) loads the
-  // 36 contiguous floats W[oc][c0 + 4h .. +4][0..9] (nine float4) and writes one 16-byte entry
-  // wl[oc][t][4h .. 4h+3] per tap. Every thread takes input task tid mod in_tasks (at most 256
-  // tasks) and weight task tid mod 128: threads that share a task write the same values, and no
+  // the padding columns stay zero from the prologue. Every thread takes input task
+  // tid mod in_tasks (at most 256 tasks): threads that share a task write the same values, and no
   // staging step is under a branch, so the compiler's wait counting keeps the loads in flight
   // across the MFMAs. Loads always use valid addresses (rows outside the image read row 0, output
   // channels past Oc read channel 0); the zero masks apply when the registers are written to LDS.
@@ -437,35 +438,60 @@ __global__ void __launch_bounds__(256)
   const bool in_ok = ihi >= 0 && ihi < a.H;
   const int64_t in_off = (int64_t)4 * iq * HW + (int64_t)(in_ok ? ihi : 0) * a.W + 4 * ig;
   float* const in_dst0 = lds + ((iq * kLdsRows + irr) * kLdsCols + a.pad + 4 * ig) * 4;
-  const int wocl = (tid & 127) >> 1, wh = tid & 1;
+  // Weight staging. PT = 1: task (oc, channel quad h) = tid mod 128 loads the 36 contiguous floats
+  // W[oc][c0 + 4h .. +4][0..9] (nine float4) and writes one 16-byte entry wl[oc][t][4h .. 4h+3]
+  // per tap. PT = 2: task (oc, channel j) = tid loads the nine floats W[oc][c0 + j][0..9] and
+  // writes them to wl[oc][t][j], so the 512 threads share the chunk's weights evenly and no
+  // register transposition is needed.
+  constexpr int kWf = PT == 1 ? 36 : 9;
+  const int wocl = PT == 1 ? (tid & 127) >> 1 : tid >> 3;
+  const int wch = PT == 1 ? 4 * (tid & 1) : tid & 7;
   const bool w_ok = oc_base + wocl < a.Oc;
-  const float* const w_src0 = a.w + ((int64_t)(w_ok ? oc_base + wocl : 0) * a.C + 4 * wh) * 9;
-  float* const w_dst0 = lds + kXlFloats + wocl * kWPitch + 4 * wh;
-  f32x4 xs[4];
-  f32x4 ws[9];
-  auto load_chunk = [&](int c0) {
+  const float* const w_src0 = a.w + ((int64_t)(w_ok ? oc_base + wocl : 0) * a.C + wch) * 9;
+  float* const w_dst0 = lds + kXlFloats + wocl * kWPitch + wch;
+  // One chunk's staging registers (PT = 2 alternates two sets, see the main loop).
+  struct Stage {
+    f32x4 xs[4];
+    float wf[kWf];
+  };
+  auto load_chunk = [&](Stage& r, int c0) {
     const float* src = xn + (int64_t)c0 * HW + in_off;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) xs[j] = *reinterpret_cast<const f32x4*>(src + j * HW);
+    for (int j = 0; j < 4; ++j) r.xs[j] = *reinterpret_cast<const f32x4*>(src + j * HW);
     const float* wsrc = w_src0 + (int64_t)c0 * 9;
+    if constexpr (PT == 1) {
 #pragma unroll
-    for (int i = 0; i < 9; ++i) ws[i] = *reinterpret_cast<const f32x4*>(wsrc + 4 * i);
+      for (int i = 0; i < 9; ++i) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(wsrc + 4 * i);
+        r.wf[4 * i] = v[0];
+        r.wf[4 * i + 1] = v[1];
+        r.wf[4 * i + 2] = v[2];
+        r.wf[4 * i + 3] = v[3];
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 9; ++t) r.wf[t] = wsrc[t];
+    }
   };
-  auto store_chunk = [&](int b) {
+  auto store_chunk = [&](const Stage& r, int b) {
     // Rows above or below the image are zero padding (a select: the loaded row may hold inf).
     float* dst = in_dst0 + b * kConvLdsBuf;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       *reinterpret_cast<f32x4*>(dst + 4 * i) =
-          in_ok ? f32x4{xs[0][i], xs[1][i], xs[2][i], xs[3][i]} : f32x4{0.f, 0.f, 0.f, 0.f};
-    // ws holds W[oc][c0 + 4 wh + j][t] at flat index 9 j + t (j < 4, t < 9). Output channels
-    // past Oc get zero weights.
+          in_ok ? f32x4{r.xs[0][i], r.xs[1][i], r.xs[2][i], r.xs[3][i]} : f32x4{0.f, 0.f, 0.f, 0.f};
+    // Output channels past Oc get zero weights.
     float* wdst = w_dst0 + b * kConvLdsBuf;
-    const float* f = reinterpret_cast<const float*>(ws);
+    if constexpr (PT == 1) {
+      // wf holds W[oc][c0 + 4 h + j][t] at index 9 j + t (j < 4, t < 9).
 #pragma unroll
-    for (int t = 0; t < 9; ++t)
-      *reinterpret_cast<f32x4*>(wdst + 8 * t) =
-          w_ok ? f32x4{f[t], f[9 + t], f[18 + t], f[27 + t]} : f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int t = 0; t < 9; ++t)
+        *reinterpret_cast<f32x4*>(wdst + 8 * t) =
+            w_ok ? f32x4{r.wf[t], r.wf[9 + t], r.wf[18 + t], r.wf[27 + t]} : f32x4{0.f, 0.f, 0.f, 0.f};
+    } else {
+#pragma unroll
+      for (int t = 0; t < 9; ++t) wdst[8 * t] = w_ok ? r.wf[t] : 0.f;
+    }
   };
 
   // This lane's pixel (column of the MFMA tile) and k half.
@@ -477,21 +503,7 @@ __global__ void __launch_bounds__(256)
   const int wbase = kXlFloats + (oh * 32 + (lane & 31)) * kWPitch + 4 * kk;
 
   f32x16 acc[4] = {f32x16{}, f32x16{}, f32x16{}, f32x16{}};
-  load_chunk(0);
-  for (int i = tid; i < 2 * kXlFloats / 4; i += 256) {  // zero padding in both input buffers
-    const int b = i / (kXlFloats / 4), e = i % (kXlFloats / 4);
-    *reinterpret_cast<f32x4*>(lds + b * kConvLdsBuf + 4 * e) = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-  __syncthreads();
-  store_chunk(0);
-  __syncthreads();
-  const int chunks = a.C / 8;
-  for (int k = 0; k < chunks; ++k) {
-    const float* cur = lds + (k & 1) * kConvLdsBuf;
-    // The next chunk's loads (the last chunk's again on the final pass: a cheap, unbranched
-    // repeat) are in flight while this chunk is multiplied.
-    load_chunk(8 * (k + 1 < chunks ? k + 1 : k));
-    __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the MFMAs
+  auto multiply = [&](const float* cur) {
 #pragma unroll
     for (int t = 0; t < 9; ++t) {
       const int kh = t / 3, kw = t % 3;
@@ -503,12 +515,52 @@ __global__ void __launch_bounds__(256)
       acc[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(wv.z, xv.z, acc[2], 0, 0, 0);
       acc[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(wv.w, xv.w, acc[3], 0, 0, 0);
     }
-    __builtin_amdgcn_sched_barrier(0);  // no use of the loaded registers ahead of the MFMAs
-    // The other buffer's last readers (chunk k - 1) all passed the previous barrier. The store
-    // is unconditional (after the last chunk it writes a buffer nobody reads) so that the
-    // loads above stay where they are instead of sinking into a branch behind the MFMAs.
-    store_chunk((k + 1) & 1);
-    if (k + 1 < chunks) __syncthreads();
+  };
+  const int chunks = a.C / 8;
+  Stage sa, sb;
+  load_chunk(sa, 0);
+  if constexpr (PT == 2) load_chunk(sb, chunks > 1 ? 8 : 0);
+  for (int i = tid; i < 2 * kXlFloats / 4; i += kThreads) {  // zero padding in both input buffers
+    const int b = i / (kXlFloats / 4), e = i % (kXlFloats / 4);
+    *reinterpret_cast<f32x4*>(lds + b * kConvLdsBuf + 4 * e) = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  __syncthreads();
+  store_chunk(sa, 0);
+  __syncthreads();
+  // In both schedules below every load and store of the loop is unconditional: a store after the
+  // last chunk writes a buffer nobody reads, and loads past the last chunk repeat it. A load or
+  // store under a branch lets the compiler sink loads behind the MFMAs, or makes its wait
+  // counting (which cannot tell that a skipped step also leaves the loop) wait for loads that
+  // should stay in flight. The other buffer's last readers (chunk k - 1) all passed the previous
+  // barrier when chunk k + 1 is written to it. (Writing it halfway through the taps instead
+  // measured slower.)
+  if constexpr (PT == 2) {
+    // Two chunks ahead: chunk k's `mine` set (already in LDS) takes chunk k + 2's loads and
+    // `next` (chunk k + 1) is written after chunk k's MFMAs. The input streams from HBM and one
+    // chunk's MFMAs do not cover its load latency. With an odd chunk count the last step
+    // (k = chunks) only repeats loads and a store.
+    auto step = [&](int k, Stage& mine, const Stage& next) {
+      load_chunk(mine, 8 * (k + 2 < chunks ? k + 2 : chunks - 1));
+      __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the MFMAs
+      if (k < chunks) multiply(lds + (k & 1) * kConvLdsBuf);
+      __builtin_amdgcn_sched_barrier(0);  // no use of the loaded registers ahead of the MFMAs
+      store_chunk(next, (k + 1) & 1);
+      if (k + 1 < chunks) __syncthreads();
+    };
+    for (int k = 0; k < chunks; k += 2) {
+      step(k, sa, sb);
+      step(k + 1, sb, sa);
+    }
+  } else {
+    // One chunk ahead (a second register set would cost the second workgroup per CU).
+    for (int k = 0; k < chunks; ++k) {
+      load_chunk(sa, 8 * (k + 1 < chunks ? k + 1 : k));
+      __builtin_amdgcn_sched_barrier(0);
+      multiply(lds + (k & 1) * kConvLdsBuf);
+      __builtin_amdgcn_sched_barrier(0);
+      store_chunk(sa, (k + 1) & 1);
+      if (k + 1 < chunks) __syncthreads();
+    }
   }
 
   // Epilogue: lane -> pixel (column), rows oc = oc_base + 32 oh + 8 (r / 4) + 4 kk + r % 4.
@@ -599,12 +651,17 @@ hipError_t launch_conv_igemm(const Plan& p, const Shape& sh, Layout lay, const f
   a.Wo = (int)sh.Wo;
   a.strips = (int)((sh.Ho * sh.Wo + 31) / 32);
   if (v.tile_strips < 0) {  // conv_lds_kernel: NCHW 3x3 stride 1, both operands staged in LDS
-    if (!conv_lds_supported(nchw, sh.Kh, sh.Kw, sh.stride, sh.pad, sh.W, sh.Ho, sh.Wo, sh.Ci)) return hipErrorInvalidValue;
+    const int pt = -v.tile_strips;
+    if (pt != 1 && pt != 2) return hipErrorInvalidValue;
+    if (!conv_lds_supported(nchw, sh.Kh, sh.Kw, sh.stride, sh.pad, sh.W, sh.Ho, sh.Wo, sh.Ci, 64 * pt))
+      return hipErrorInvalidValue;
     if ((((uintptr_t)X) | ((uintptr_t)Wt)) & 15) return hipErrorInvalidValue;
-    const int64_t tiles = (sh.Ho * sh.Wo + 63) / 64;
+    const int64_t tiles = (sh.Ho * sh.Wo + 64 * pt - 1) / (64 * pt);
     const int oc_tiles = (int)((sh.Co + 63) / 64);
     if (sh.Nb * tiles > INT32_MAX || oc_tiles > 65535) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(kern::conv_lds_kernel, dim3((unsigned)(sh.Nb * tiles), (unsigned)oc_tiles), dim3(256), 0, s, a);
+    const dim3 grid((unsigned)(sh.Nb * tiles), (unsigned)oc_tiles);
+    if (pt == 1) hipLaunchKernelGGL(kern::conv_lds_kernel<1>, grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(kern::conv_lds_kernel<2>, grid, dim3(512), 0, s, a);
     return hipGetLastError();
   }
   if (v.tile_strips > 0) {  // 32 x 32 wavefront tiles, chunked coalesced weight staging

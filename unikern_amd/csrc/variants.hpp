@@ -99,8 +99,8 @@ constexpr int kNumQ8Variants = sizeof(kQ8Variants) / sizeof(kQ8Variants[0]);
 // bk_bytes is the LDS budget of one staged weight chunk (channels = budget / (taps * 64 * 4 B),
 // even). Tile kernel (tile_strips S > 0, 3x3 and 1x1 only): wavefronts of 32 pixels x 32 output
 // channels, S strips x 2 channel halves per workgroup, bk_bytes channels per weight chunk. LDS
-// kernel (tile_strips -1, NCHW 3x3 stride 1 only, see conv_lds_supported): 64 pixels x 64
-// output channels per workgroup of four wavefronts, input rows and weights of 8 channels staged
+// kernel (tile_strips -T, NCHW 3x3 stride 1 only, see conv_lds_supported): 64 T pixels x 64
+// output channels per workgroup of 4 T wavefronts, input rows and weights of 8 channels staged
 // in LDS. eff is the calibrated fraction of the f32 MFMA rate the busiest SIMD sustains
 // (kernel-only median at the BASELINE conv shape on one MI355X).
 struct ConvVariant {
@@ -112,17 +112,19 @@ struct ConvVariant {
 constexpr ConvVariant kConvVariants[] = {
     {4, 147456, 0, 0.273}, {2, 73728, 0, 0.175}, {4, 73728, 0, 0.260}, {2, 36864, 0, 0.170},
     {4, 16, 2, 0.130},     {4, 8, 2, 0.130},     {8, 8, 4, 0.310},     {4, 8, -1, 0.466},
+    {8, 8, -2, 0.542},
 };
 // LDS kernel geometry: input rows and padded columns one staged tile holds.
 constexpr int kConvLdsRows = 8;
 constexpr int kConvLdsCols = 64;
 // The LDS kernel covers NCHW, 3x3, stride 1, pad 0 or 1, W + 2 pad <= kConvLdsCols, W a multiple
-// of 4 and C of 8 (16-byte staging loads, whole channel chunks), and 64 consecutive output pixels
-// spanning at most kConvLdsRows - 2 output rows.
-inline bool conv_lds_supported(bool nchw, long kh, long kw, long stride, long pad, long W, long Ho, long Wo, long C) {
+// of 4 and C of 8 (16-byte staging loads, whole channel chunks), and pix (64 or 128) consecutive
+// output pixels spanning at most kConvLdsRows - 2 output rows.
+inline bool conv_lds_supported(bool nchw, long kh, long kw, long stride, long pad, long W, long Ho, long Wo, long C,
+                               long pix) {
   if (!nchw || kh != 3 || kw != 3 || stride != 1 || (pad != 0 && pad != 1)) return false;
   if (W + 2 * pad > kConvLdsCols || W % 4 != 0 || C % 8 != 0 || C <= 0 || Wo <= 0 || Ho <= 0) return false;
-  return (63 + Wo - 1) / Wo + 1 + 2 <= kConvLdsRows;
+  return (pix - 1 + Wo - 1) / Wo + 1 + 2 <= kConvLdsRows;
 }
 constexpr int kNumConvVariants = sizeof(kConvVariants) / sizeof(kConvVariants[0]);
 
