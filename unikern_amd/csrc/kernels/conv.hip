@@ -422,75 +422,95 @@ __global__ void __launch_bounds__(256 * PT)
   const float* xn = a.x + (int64_t)n * a.C * a.H * a.W;
   const int64_t HW = (int64_t)a.H * a.W;
 
-  // Input staging, with 16-byte global loads: task (quad q, row rr, column group g) loads the
-  // four channels of the quad at input columns 4g .. 4g+3 of one row (four float4 loads along W),
-  // transposes them in registers and writes four 16-byte entries [q][rr][pad + 4g + i][0..3];
-  // the padding columns stay zero from the prologue. Every thread takes input task
-  // tid mod in_tasks (at most 256 tasks): threads that share a task write the same values, and no
-  // staging step is under a branch, so the compiler's wait counting keeps the loads in flight
-  // across the MFMAs. Loads always use valid addresses (rows outside the image read row 0, output
-  // channels past Oc read channel 0); the zero masks apply when the registers are written to LDS.
-  const int groups = a.W / 4;
+  // Input staging: task (quad q, row rr, column group g) loads the four channels of the quad at
+  // input columns kXW g .. kXW g + kXW - 1 of one row (four vector loads along W, one per
+  // channel), transposes them in registers and writes kXW 16-byte entries
+  // [q][rr][pad + kXW g + i][0..3]; the padding columns stay zero from the prologue. PT = 1 takes
+  // four columns (at most 256 tasks for 256 threads); PT = 2 two columns (at most 512 tasks for
+  // 512 threads), so adjacent lanes write entries 32 bytes apart instead of 64 (2-way instead of
+  // 4-way bank conflicts) and fewer threads repeat a task. Every thread takes input task
+  // tid mod in_tasks: threads that share a task write the same values, and no staging step is
+  // under a branch, so the compiler's wait counting keeps the loads in flight across the MFMAs.
+  // Loads always use valid addresses (rows outside the image read row 0, output channels past
+  // Oc read channel 0); the zero masks apply when the registers are written to LDS.
+  constexpr int kXW = PT == 1 ? 4 : 2;
+  const int groups = a.W / kXW;
   const int it = tid % (2 * in_rows * groups);
   const int iq = it / (in_rows * groups);
   const int irr = (it / groups) % in_rows, ig = it % groups;
   const int ihi = r0 + irr - a.pad;
   const bool in_ok = ihi >= 0 && ihi < a.H;
-  const int64_t in_off = (int64_t)4 * iq * HW + (int64_t)(in_ok ? ihi : 0) * a.W + 4 * ig;
-  float* const in_dst0 = lds + ((iq * kLdsRows + irr) * kLdsCols + a.pad + 4 * ig) * 4;
+  const int64_t in_off = (int64_t)4 * iq * HW + (int64_t)(in_ok ? ihi : 0) * a.W + kXW * ig;
+  float* const in_dst0 = lds + ((iq * kLdsRows + irr) * kLdsCols + a.pad + kXW * ig) * 4;
   // Weight staging. PT = 1: task (oc, channel quad h) = tid mod 128 loads the 36 contiguous floats
   // W[oc][c0 + 4h .. +4][0..9] (nine float4) and writes one 16-byte entry wl[oc][t][4h .. 4h+3]
   // per tap. PT = 2: task (oc, channel j) = tid loads the nine floats W[oc][c0 + j][0..9] and
   // writes them to wl[oc][t][j], so the 512 threads share the chunk's weights evenly and no
   // register transposition is needed.
-  constexpr int kWf = PT == 1 ? 36 : 9;
+  constexpr int kWv = PT == 1 ? 9 : 2;  // float4 registers per weight task (PT = 2: plus one float)
   const int wocl = PT == 1 ? (tid & 127) >> 1 : tid >> 3;
   const int wch = PT == 1 ? 4 * (tid & 1) : tid & 7;
   const bool w_ok = oc_base + wocl < a.Oc;
   const float* const w_src0 = a.w + ((int64_t)(w_ok ? oc_base + wocl : 0) * a.C + wch) * 9;
   float* const w_dst0 = lds + kXlFloats + wocl * kWPitch + wch;
   // One chunk's staging registers (PT = 2 alternates two sets, see the main loop).
+  // Members are float4 vectors (for PT = 2 the input uses two lanes of each, the weights nine
+  // floats of wv and wl): arrays of floats or float2, filled and read through vectors of another
+  // width, kept the staging registers in scratch memory.
   struct Stage {
     f32x4 xs[4];
-    float wf[kWf];
+    f32x4 wv[kWv];
+    float wl;
   };
-  auto load_chunk = [&](Stage& r, int c0) {
+  auto load_chunk = [&](Stage& r, int c0) __attribute__((always_inline)) {
     const float* src = xn + (int64_t)c0 * HW + in_off;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) r.xs[j] = *reinterpret_cast<const f32x4*>(src + j * HW);
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (kXW == 4) {
+        r.xs[j] = *reinterpret_cast<const f32x4*>(src + j * HW);
+      } else {
+        const f32x2 v = *reinterpret_cast<const f32x2*>(src + j * HW);
+        r.xs[j] = f32x4{v.x, v.y, 0.f, 0.f};
+      }
+    }
     const float* wsrc = w_src0 + (int64_t)c0 * 9;
     if constexpr (PT == 1) {
 #pragma unroll
-      for (int i = 0; i < 9; ++i) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(wsrc + 4 * i);
-        r.wf[4 * i] = v[0];
-        r.wf[4 * i + 1] = v[1];
-        r.wf[4 * i + 2] = v[2];
-        r.wf[4 * i + 3] = v[3];
-      }
+      for (int i = 0; i < 9; ++i) r.wv[i] = *reinterpret_cast<const f32x4*>(wsrc + 4 * i);
     } else {
-#pragma unroll
-      for (int t = 0; t < 9; ++t) r.wf[t] = wsrc[t];
+      // W[oc][c0 + j][0..9] is 4-byte aligned; the compiler merges the nine loads.
+      r.wv[0] = f32x4{wsrc[0], wsrc[1], wsrc[2], wsrc[3]};
+      r.wv[1] = f32x4{wsrc[4], wsrc[5], wsrc[6], wsrc[7]};
+      r.wl = wsrc[8];
     }
   };
-  auto store_chunk = [&](const Stage& r, int b) {
+  auto store_chunk = [&](const Stage& r, int b) __attribute__((always_inline)) {
     // Rows above or below the image are zero padding (a select: the loaded row may hold inf).
     float* dst = in_dst0 + b * kConvLdsBuf;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<f32x4*>(dst + 4 * i) =
-          in_ok ? f32x4{r.xs[0][i], r.xs[1][i], r.xs[2][i], r.xs[3][i]} : f32x4{0.f, 0.f, 0.f, 0.f};
+    auto entry = [&](int i, f32x4 v) __attribute__((always_inline)) {
+      *reinterpret_cast<f32x4*>(dst + 4 * i) = in_ok ? v : f32x4{0.f, 0.f, 0.f, 0.f};
+    };
+    entry(0, f32x4{r.xs[0].x, r.xs[1].x, r.xs[2].x, r.xs[3].x});
+    entry(1, f32x4{r.xs[0].y, r.xs[1].y, r.xs[2].y, r.xs[3].y});
+    if constexpr (kXW == 4) {
+      entry(2, f32x4{r.xs[0].z, r.xs[1].z, r.xs[2].z, r.xs[3].z});
+      entry(3, f32x4{r.xs[0].w, r.xs[1].w, r.xs[2].w, r.xs[3].w});
+    }
     // Output channels past Oc get zero weights.
     float* wdst = w_dst0 + b * kConvLdsBuf;
     if constexpr (PT == 1) {
-      // wf holds W[oc][c0 + 4 h + j][t] at index 9 j + t (j < 4, t < 9).
+      // Flat float i of wv is W[oc][c0 + 4 h + i / 9][i % 9].
+      auto f = [&](int i) { return r.wv[i >> 2][i & 3]; };
 #pragma unroll
       for (int t = 0; t < 9; ++t)
         *reinterpret_cast<f32x4*>(wdst + 8 * t) =
-            w_ok ? f32x4{r.wf[t], r.wf[9 + t], r.wf[18 + t], r.wf[27 + t]} : f32x4{0.f, 0.f, 0.f, 0.f};
+            w_ok ? f32x4{f(t), f(9 + t), f(18 + t), f(27 + t)} : f32x4{0.f, 0.f, 0.f, 0.f};
     } else {
 #pragma unroll
-      for (int t = 0; t < 9; ++t) wdst[8 * t] = w_ok ? r.wf[t] : 0.f;
+      for (int t = 0; t < 9; ++t) {
+        const float v = t < 4 ? r.wv[0][t & 3] : t < 8 ? r.wv[1][t & 3] : r.wl;  // t is a constant here
+        wdst[8 * t] = w_ok ? v : 0.f;
+      }
     }
   };
 
@@ -503,7 +523,7 @@ __global__ void __launch_bounds__(256 * PT)
   const int wbase = kXlFloats + (oh * 32 + (lane & 31)) * kWPitch + 4 * kk;
 
   f32x16 acc[4] = {f32x16{}, f32x16{}, f32x16{}, f32x16{}};
-  auto multiply = [&](const float* cur) {
+  auto multiply = [&](const float* cur) __attribute__((always_inline)) {
 #pragma unroll
     for (int t = 0; t < 9; ++t) {
       const int kh = t / 3, kw = t % 3;
@@ -539,7 +559,7 @@ __global__ void __launch_bounds__(256 * PT)
     // `next` (chunk k + 1) is written after chunk k's MFMAs. The input streams from HBM and one
     // chunk's MFMAs do not cover its load latency. With an odd chunk count the last step
     // (k = chunks) only repeats loads and a store.
-    auto step = [&](int k, Stage& mine, const Stage& next) {
+    auto step = [&](int k, Stage& mine, const Stage& next) __attribute__((always_inline)) {
       load_chunk(mine, 8 * (k + 2 < chunks ? k + 2 : chunks - 1));
       __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the MFMAs
       if (k < chunks) multiply(lds + (k & 1) * kConvLdsBuf);
