@@ -737,6 +737,7 @@ int uk_solve(const char* hcs_json, const uk_op_desc* d, uk_plan* out, char* log,
   os << "SOLVE family=" << to_string(p->family) << " key=" << p->key << " predicted_us=" << p->predicted_us
      << " feasible=" << p->feasible << " why=" << p->why;
   for (const auto& r : sl.rejected) os << "\n  rejected " << r;
+  for (const auto& [us, key] : sl.ranked) os << "\n  candidate " << key << " predicted_us=" << us;
   put(os.str(), log, cap);
   return UK_OK;
 }

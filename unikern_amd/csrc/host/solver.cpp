@@ -89,7 +89,7 @@ std::string fmt(const char* f, double a) {
   return b;
 }
 
-std::optional<Plan> pick(std::vector<Cand>& cs, const char* family_name, std::string* err) {
+std::optional<Plan> pick(std::vector<Cand>& cs, const char* family_name, SolveLog* log, std::string* err) {
   if (cs.empty()) {
     if (err) *err = std::string("no feasible ") + family_name + " candidate";
     return std::nullopt;
@@ -97,6 +97,10 @@ std::optional<Plan> pick(std::vector<Cand>& cs, const char* family_name, std::st
   const Cand* best = &cs[0];
   for (const Cand& c : cs)
     if (c.cost < best->cost || (c.cost == best->cost && c.plan.key < best->plan.key)) best = &c;
+  if (log) {
+    for (const Cand& c : cs) log->ranked.emplace_back(c.cost, c.plan.key);
+    std::sort(log->ranked.begin(), log->ranked.end());
+  }
   Plan p = best->plan;
   p.predicted_us = best->cost;
   p.feasible = int(cs.size());
@@ -154,7 +158,7 @@ std::optional<Plan> solve_rows(const Hcs& h, const KmlTree& t, const Shape& s, S
     c.cost = cost;
     cs.push_back(c);
   }
-  if (!cs.empty()) return pick(cs, "rows", err);
+  if (!cs.empty()) return pick(cs, "rows", log, err);
   // Fallback for any row length: stream the row.
   Plan p;
   p.family = Family::RowsStream;
@@ -256,10 +260,12 @@ std::optional<Plan> solve_gemm(const Hcs& h, const KmlTree& t, const Shape& s, S
     c.cost = launch_us(h) + flops / (peak_tflops * 1e6 * 0.12) + 1.0;
     cs.push_back(c);
   }
-  return pick(cs, "gemm", err);
+  return pick(cs, "gemm", log, err);
 }
 
 // ---------------------------------------------------------------------------------------
+constexpr double kActBytesPerUsPerCu = 74e3;  // activation bytes per us per CU and round (fitted)
+
 std::optional<Plan> solve_q8(const Hcs& h, const KmlTree& t, const Shape& s, SolveLog* log, std::string* err) {
   const Workload w = workload_of(t);
   std::vector<Cand> cs;
@@ -268,7 +274,8 @@ std::optional<Plan> solve_q8(const Hcs& h, const KmlTree& t, const Shape& s, Sol
     const Q8Variant v = kQ8Variants[i];
     std::ostringstream key;
     key << "q8_0:waves=" << v.waves << ",pairs=" << v.pairs << ",vec=" << v.vec << (v.db ? ",db" : "");
-    const int64_t lds = int64_t(v.waves) * v.pairs * 16 * 17 * 4 * (v.db ? 2 : 1);
+    if (v.nt > 1) key << ",nt=" << v.nt;
+    const int64_t lds = int64_t(v.waves) * v.nt * v.pairs * 16 * 17 * 4 * (v.db ? 2 : 1);
     if (v.vec == 4 && s.K % (64 * v.pairs) != 0) {
       reject(log, key.str() + " violates K%(64*pairs)==0 (16-byte aligned copies)");
       continue;
@@ -281,11 +288,11 @@ std::optional<Plan> solve_q8(const Hcs& h, const KmlTree& t, const Shape& s, Sol
     const int64_t rounds = (npairs + per_round - 1) / per_round;
     // Pairs of the last round beyond K/64 are copied and skipped: wasted bandwidth.
     const double useful = double(npairs) / double(rounds * per_round);
-    const int64_t grid = ((s.N + 15) / 16) * ((s.M + 15) / 16);
+    const int64_t grid = ((s.N + 16 * v.nt - 1) / (16 * v.nt)) * ((s.M + 15) / 16);
     const int wps = waves_by_regs(h, 96);
     const int resident = std::max(1, std::min<int>(wps * simds(h) / v.waves, int(lds_cu(h) / lds)));
     // Bytes in flight per workgroup: one round of copies (two with double buffering).
-    const double inflight = double(per_round) * 16.0 * 68.0 * useful * (v.db && rounds > 1 ? 2.0 : 1.0);
+    const double inflight = double(per_round) * 16.0 * v.nt * 68.0 * useful * (v.db && rounds > 1 ? 2.0 : 1.0);
     // Copy instructions: 16-byte copies issue a quarter of the dword ones.
     const double issue_us = double(rounds) * (v.vec == 4 ? 0.3 : 1.2);
     // Each generation of resident workgroups waits one load latency before its first round
@@ -294,8 +301,16 @@ std::optional<Plan> solve_q8(const Hcs& h, const KmlTree& t, const Shape& s, Sol
     const int64_t slots = int64_t(cus(h)) * resident;
     const int64_t generations = (grid + slots - 1) / slots;
     const double gen_us = double(generations) * 0.5 * kMemLatencyUs;
-    const double cost =
-        launch_us(h) + stream_us(h, double(w.bytes) / useful, grid, resident, inflight) + issue_us + gen_us;
+    // Every workgroup reads its activation rows over all of K (from L2); the n-tiles of a
+    // workgroup share each activation fragment. Fitted over the variants at the BASELINE shapes:
+    // the busiest CU's activation bytes cost about 1 us per 74 KB for each round of a wavefront
+    // (a round's wait covers its activation loads with its copies), and without double
+    // buffering every round after the first exposes half a load latency.
+    const double act_cu = std::ceil(double(grid) / cus(h)) * double(std::min<int64_t>(s.M, 16)) * double(s.K) * 2.0;
+    const double act_us = act_cu * double(rounds) / kActBytesPerUsPerCu;
+    const double rounds_us = v.db ? 0.0 : double(rounds - 1) * 0.5 * kMemLatencyUs;
+    const double cost = launch_us(h) + stream_us(h, double(w.bytes) / useful, grid, resident, inflight) + issue_us +
+                        gen_us + act_us + rounds_us;
     Cand c;
     c.plan.family = Family::Q8Gemm;
     c.plan.variant = i;
@@ -304,13 +319,13 @@ std::optional<Plan> solve_q8(const Hcs& h, const KmlTree& t, const Shape& s, Sol
     c.plan.tile_k = int(per_round * 64);
     c.plan.grid = grid;
     c.plan.key = key.str();
-    c.plan.why = std::to_string(grid) + " workgroups of 16 weight rows, " + std::to_string(rounds) +
+    c.plan.why = std::to_string(grid) + " workgroups of " + std::to_string(16 * v.nt) + " weight rows, " + std::to_string(rounds) +
                  " round(s) of " + std::to_string(per_round) + " block pairs, " + std::to_string(resident) +
                  " resident per CU";
     c.cost = cost;
     cs.push_back(c);
   }
-  return pick(cs, "q8_0", err);
+  return pick(cs, "q8_0", log, err);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -397,7 +412,7 @@ std::optional<Plan> solve_conv(const Hcs& h, const KmlTree& t, const Shape& s, S
     c.cost = cost;
     cs.push_back(c);
   }
-  return pick(cs, "conv", err);
+  return pick(cs, "conv", log, err);
 }
 
 }  // namespace

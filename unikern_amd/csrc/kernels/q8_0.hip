@@ -25,7 +25,10 @@
 // lane's outputs all belong to one weight row and its two block scales are one LDS broadcast.
 //
 // K must be a multiple of 64 (whole block pairs per row).
-// Work split: grid.x = 16-row groups of weights, grid.y = 16-row groups of activations. A round
+// Work split: grid.x = groups of 16 NT weight rows, grid.y = 16-row groups of activations. With
+// NT > 1 each activation fragment (read from global memory per workgroup) feeds NT MFMA tiles of
+// weights: every workgroup reads all of its activation rows over K, so for M = 16 the activation
+// reads (M K 2 bytes per workgroup, from L2) exceed the workgroup's weight bytes at NT = 1. A round
 // covers WAVES * P pairs; wavefront w takes pairs [w * P, w * P + P) of it. Each wavefront
 // accumulates in registers across rounds; the partials fold in LDS in wavefront order
 // (deterministic). Weight rows past N read row n0 (valid memory) and are never stored;
@@ -69,22 +72,22 @@ __device__ __forceinline__ void q8_wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <int WAVES, int P, int VEC, bool DB>
+template <int WAVES, int P, int VEC, bool DB, int NT>
 __global__ void __launch_bounds__(WAVES * 64)
     q8_0_gemm_kernel(const _Float16* __restrict__ X, const uint8_t* __restrict__ Wq, float* __restrict__ Y, int M,
                      int N, int K) {
   static_assert(VEC == 1 || (VEC == 4 && P % 4 == 0), "16-byte copies need 16-byte aligned segments");
   constexpr int kRowDw = 17 * P;                   // one row's P block pairs, in dwords
-  constexpr int kWaveDw = 16 * kRowDw;             // this wavefront's staging area
+  constexpr int kWaveDw = NT * 16 * kRowDw;        // this wavefront's staging area
   constexpr int kUnits = kWaveDw / VEC;            // copy units of VEC dwords
   constexpr int kInst = (kUnits + 63) / 64;        // DMA instructions per round
   static_assert(2 * (2 * P + kInst) <= 63, "two rounds of loads must fit the vmcnt counter");
-  static_assert(WAVES * kWaveDw >= WAVES * 256, "the partials fold reuses the staging buffer");
+  static_assert(WAVES * kWaveDw >= WAVES * 256 * NT, "the partials fold reuses the staging buffer");
   __shared__ uint32_t wl[WAVES * kWaveDw * (DB ? 2 : 1)];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int i = lane & 15, g = lane >> 4;
-  const int n0 = blockIdx.x * 16, m0 = blockIdx.y * 16;
+  const int n0 = blockIdx.x * 16 * NT, m0 = blockIdx.y * 16;
   const int npairs = K >> 6;
   const int64_t row_bytes = (int64_t)npairs * 68;
   uint32_t* mine = wl + wave * kWaveDw * (DB ? 2 : 1);
@@ -108,7 +111,9 @@ __global__ void __launch_bounds__(WAVES * 64)
   const bool mok = m < M;
   const _Float16* xrow = X + (int64_t)(mok ? m : 0) * K + 8 * g;
 
-  f32x4 yacc = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 yacc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) yacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   const f32x4 zero = f32x4{0.f, 0.f, 0.f, 0.f};
   // Round issue: the activations of this wavefront's pairs p0 .. p0 + P - 1, then the weight
   // copies into `buf`. Pairs past K/64 read pair 0 (valid memory) and are skipped below.
@@ -134,32 +139,35 @@ __global__ void __launch_bounds__(WAVES * 64)
     }
   };
   auto compute = [&](int p0, const uint32_t* buf, const f16x8 (&xa)[P], const f16x8 (&xb)[P]) {
-    const uint32_t* lrow = buf + i * kRowDw;
 #pragma unroll
     for (int j = 0; j < P; ++j) {
       const int p = p0 + j;
       if (p >= npairs) break;  // wave-uniform: the last round's tail
-      const uint32_t* pw = lrow + 17 * j;
-      const uint32_t a0 = pw[2 * g], a1 = pw[2 * g + 1];
-      const uint32_t a2 = pw[2 * g + 2];  // dword 8 also carries the odd block's scale (lanes g = 3)
-      const uint32_t b0 = pw[9 + 2 * g], b1 = pw[10 + 2 * g];
       const f16x8 x0 = mok ? xa[j] : f16x8{};
       const f16x8 x1 = mok ? xb[j] : f16x8{};
-      // Even block: quant bytes 2..9 of this lane's 12-byte window; odd block: aligned.
-      const f16x8 qa = q8_to_f16x8(__builtin_amdgcn_alignbyte(a1, a0, 2), __builtin_amdgcn_alignbyte(a2, a1, 2));
-      const f16x8 qb = q8_to_f16x8(b0, b1);
-      // A = activations (row m = i), B = quants (column n = i): the output lanes (i, g) hold
-      // C[m = 4g + r][n = i], so every lane's four outputs belong to weight row i and need only
-      // that row's two block scales, read as an LDS broadcast (dword 0: d_even in the low half,
-      // dword 8: d_odd in the high half).
-      const f32x4 s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0, qa, zero, 0, 0, 0);
-      const f32x4 s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1, qb, zero, 0, 0, 0);
-      const float d0 = half_bits_to_float(pw[0]);
-      const float d1 = half_bits_to_float(pw[8] >> 16);
+      // The pair's activations serve the NT 16-row tiles of weights.
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        yacc[r] = fmaf(d0, s0[r], yacc[r]);
-        yacc[r] = fmaf(d1, s1[r], yacc[r]);
+      for (int t = 0; t < NT; ++t) {
+        const uint32_t* pw = buf + (t * 16 + i) * kRowDw + 17 * j;
+        const uint32_t a0 = pw[2 * g], a1 = pw[2 * g + 1];
+        const uint32_t a2 = pw[2 * g + 2];  // dword 8 also carries the odd block's scale (lanes g = 3)
+        const uint32_t b0 = pw[9 + 2 * g], b1 = pw[10 + 2 * g];
+        // Even block: quant bytes 2..9 of this lane's 12-byte window; odd block: aligned.
+        const f16x8 qa = q8_to_f16x8(__builtin_amdgcn_alignbyte(a1, a0, 2), __builtin_amdgcn_alignbyte(a2, a1, 2));
+        const f16x8 qb = q8_to_f16x8(b0, b1);
+        // A = activations (row m = i), B = quants (column n = i): the output lanes (i, g) hold
+        // C[m = 4g + r][n = i], so every lane's four outputs belong to weight row i and need only
+        // that row's two block scales, read as an LDS broadcast (dword 0: d_even in the low half,
+        // dword 8: d_odd in the high half).
+        const f32x4 s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0, qa, zero, 0, 0, 0);
+        const f32x4 s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1, qb, zero, 0, 0, 0);
+        const float d0 = half_bits_to_float(pw[0]);
+        const float d1 = half_bits_to_float(pw[8] >> 16);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          yacc[t][r] = fmaf(d0, s0[r], yacc[t][r]);
+          yacc[t][r] = fmaf(d1, s1[r], yacc[t][r]);
+        }
       }
     }
   };
@@ -205,17 +213,22 @@ __global__ void __launch_bounds__(WAVES * 64)
   float* red = reinterpret_cast<float*>(wl);
   __syncthreads();
 #pragma unroll
-  for (int r = 0; r < 4; ++r) red[wave * 256 + lane * 4 + r] = yacc[r];
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[(wave * NT + t) * 256 + lane * 4 + r] = yacc[t][r];
   __syncthreads();
   if (wave != 0) return;
-  const int n = n0 + i;  // MFMA output column = weight row
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    float s = red[lane * 4 + r];
+  for (int t = 0; t < NT; ++t) {
+    const int n = n0 + t * 16 + i;  // MFMA output column = weight row
 #pragma unroll
-    for (int w = 1; w < WAVES; ++w) s += red[w * 256 + lane * 4 + r];
-    const int mr = m0 + 4 * g + r;  // MFMA output row = activation row
-    if (n < N && mr < M) Y[(int64_t)mr * N + n] = s;
+    for (int r = 0; r < 4; ++r) {
+      float s = red[t * 256 + lane * 4 + r];
+#pragma unroll
+      for (int w = 1; w < WAVES; ++w) s += red[(w * NT + t) * 256 + lane * 4 + r];
+      const int mr = m0 + 4 * g + r;  // MFMA output row = activation row
+      if (n < N && mr < M) Y[(int64_t)mr * N + n] = s;
+    }
   }
 }
 
@@ -224,10 +237,10 @@ __global__ void __launch_bounds__(WAVES * 64)
 namespace uk {
 
 namespace {
-template <int WAVES, int P, int VEC, bool DB>
+template <int WAVES, int P, int VEC, bool DB, int NT>
 hipError_t q8_go(const void* X, const void* Wq, float* Y, int64_t M, int64_t N, int64_t K, hipStream_t s) {
-  const dim3 grid((unsigned)((N + 15) / 16), (unsigned)((M + 15) / 16));
-  hipLaunchKernelGGL((kern::q8_0_gemm_kernel<WAVES, P, VEC, DB>), grid, dim3(WAVES * 64), 0, s,
+  const dim3 grid((unsigned)((N + 16 * NT - 1) / (16 * NT)), (unsigned)((M + 15) / 16));
+  hipLaunchKernelGGL((kern::q8_0_gemm_kernel<WAVES, P, VEC, DB, NT>), grid, dim3(WAVES * 64), 0, s,
                      static_cast<const _Float16*>(X), static_cast<const uint8_t*>(Wq), Y, (int)M, (int)N, (int)K);
   return hipGetLastError();
 }
@@ -248,15 +261,17 @@ hipError_t launch_q8_gemm(const Plan& p, const void* X, const void* Wq, float* Y
   const Q8Variant v = kQ8Variants[p.variant];
   // 16-byte copies: every wavefront segment (64 P elements of K) starts 16-byte aligned.
   if (v.vec == 4 && ((K % (64 * v.pairs)) != 0 || (((uintptr_t)Wq) & 15))) return hipErrorInvalidValue;
-#define UK_Q8_CASE(W, PV, VV, DBV) \
-  if (v.waves == W && v.pairs == PV && v.vec == VV && v.db == DBV) return q8_go<W, PV, VV, DBV != 0>(X, Wq, Y, M, N, K, s);
-  UK_Q8_CASE(16, 4, 4, 0)
-  UK_Q8_CASE(16, 4, 1, 0)
-  UK_Q8_CASE(8, 8, 4, 0)
-  UK_Q8_CASE(8, 4, 1, 0)
-  UK_Q8_CASE(8, 4, 4, 1)
-  UK_Q8_CASE(4, 4, 4, 1)
-  UK_Q8_CASE(4, 8, 4, 1)
+#define UK_Q8_CASE(W, PV, VV, DBV, NTV)                                                          \
+  if (v.waves == W && v.pairs == PV && v.vec == VV && v.db == DBV && v.nt == NTV) \
+    return q8_go<W, PV, VV, DBV != 0, NTV>(X, Wq, Y, M, N, K, s);
+  UK_Q8_CASE(16, 4, 4, 0, 1)
+  UK_Q8_CASE(16, 4, 1, 0, 1)
+  UK_Q8_CASE(8, 8, 4, 0, 1)
+  UK_Q8_CASE(8, 4, 1, 0, 1)
+  UK_Q8_CASE(8, 4, 4, 1, 1)
+  UK_Q8_CASE(4, 4, 4, 1, 1)
+  UK_Q8_CASE(4, 8, 4, 1, 1)
+  UK_Q8_CASE(8, 4, 4, 0, 4)
 #undef UK_Q8_CASE
   return hipErrorInvalidValue;
 }

@@ -82,16 +82,17 @@ constexpr int kNumGemmF16Variants = sizeof(kGemmF16Variants) / sizeof(kGemmF16Va
 // Generic MFMA GEMM (any M, N, K; NT or TN; fp16 or fp32 inputs): 64x64 tiles, 4 waves.
 constexpr int kGemmGenericTile = 64;
 
-// Q8_0 skinny GEMM: a workgroup owns 16 weight rows; each of its wavefronts copies `pairs`
-// block pairs of those rows per round into its own LDS area (pairs * 1088 bytes) and computes
-// them; a round covers waves * pairs block pairs. vec: dwords per lane per copy instruction
-// (4 needs K divisible by 64 * pairs). db: two LDS buffers per wavefront, the next round's copies
-// in flight while the current round is computed.
+// Q8_0 skinny GEMM: a workgroup owns 16 nt weight rows; each of its wavefronts copies `pairs`
+// block pairs of those rows per round into its own LDS area (nt * pairs * 1088 bytes) and
+// computes them; a round covers waves * pairs block pairs. vec: dwords per lane per copy
+// instruction (4 needs K divisible by 64 * pairs). db: two LDS buffers per wavefront, the next
+// round's copies in flight while the current round is computed. nt: 16-row weight tiles that
+// share each activation fragment.
 struct Q8Variant {
-  int waves, pairs, vec, db;
+  int waves, pairs, vec, db, nt;
 };
-constexpr Q8Variant kQ8Variants[] = {{16, 4, 4, 0}, {16, 4, 1, 0}, {8, 8, 4, 0}, {8, 4, 1, 0},
-                                     {8, 4, 4, 1},  {4, 4, 4, 1},  {4, 8, 4, 1}};
+constexpr Q8Variant kQ8Variants[] = {{16, 4, 4, 0, 1}, {16, 4, 1, 0, 1}, {8, 8, 4, 0, 1}, {8, 4, 1, 0, 1},
+                                     {8, 4, 4, 1, 1},  {4, 4, 4, 1, 1},  {4, 8, 4, 1, 1}, {8, 4, 4, 0, 4}};
 constexpr int kNumQ8Variants = sizeof(kQ8Variants) / sizeof(kQ8Variants[0]);
 
 // Implicit-GEMM conv on f32 MFMA (v_mfma_f32_32x32x2f32). Wide kernel (tile_strips 0): a
