@@ -106,6 +106,35 @@ def test_f32_generic(gpu, M, N, K, layout):
     assert frob(C, R) <= 1e-5
 
 
+@pytest.mark.parametrize("vi", [0, 1])
+@pytest.mark.parametrize("M,N,K", [(64, 64, 64), (128, 192, 320), (256, 128, 512)])
+@pytest.mark.parametrize("layout", ["NT", "TN"])
+def test_f32_variants(gpu, vi, M, N, K, layout):
+    # variant 0: bounds-checked generic kernel; 1: the LDS-tiled kernel (one and several tiles,
+    # one and an odd number of k-tiles); tolerance and exact mode
+    p = gpu.Plan()
+    p.family, p.variant = 6, vi
+    A = O.uniform(M * K, 5 + M + vi, -1.0, 1.0).reshape(M, K)
+    B = O.uniform(N * K, 6 + N + vi, -1.0, 1.0).reshape((N, K) if layout == "TN" else (K, N))
+    C = gemm_gpu(gpu, A, B, "fp32", layout, plan=p)
+    assert frob(C, O.gemm_f32(A, B, layout == "TN")) <= 1e-5
+    A = O.sawtooth(M * K, 17, 8).reshape(M, K)
+    B = O.sawtooth(N * K, 13, 6).reshape((N, K) if layout == "TN" else (K, N))
+    C = gemm_gpu(gpu, A, B, "fp32", layout, plan=p)
+    assert np.array_equal(C.view(np.uint32), O.gemm_f32(A, B, layout == "TN").view(np.uint32))
+
+
+def test_f32_tiled_refuses_other_shapes(gpu):
+    p = gpu.Plan()
+    p.family, p.variant = 6, 1
+    A = O.uniform(64 * 96, 1, -1.0, 1.0).reshape(64, 96)  # K = 96 is not a multiple of 64
+    B = O.uniform(96 * 64, 2, -1.0, 1.0).reshape(96, 64)
+    with pytest.raises(gpu.UnikernError):
+        gemm_gpu(gpu, A, B, "fp32", "NT", plan=p)
+    assert gpu.solve(gpu.make_desc("gemm", [1024, 1024, 1024], dtype="fp32", layout="NT")).key == "gemm_f32:64x64x64,w8"
+    assert gpu.solve(gpu.make_desc("gemm", [64, 64, 96], dtype="fp32", layout="NT")).key == "gemm_generic:64x64x16"
+
+
 def test_f32_exact_mode_reference_sample_shape(gpu):
     # samples/kml_gemm.json (512^3, NT) on the reference's sawtooth: bit-exact.
     M = N = K = 512

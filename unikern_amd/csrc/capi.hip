@@ -220,7 +220,7 @@ int dispatch(const KmlTree& t, const Plan& p, const void* const* in, void* out, 
       else if (p.family == Family::GemmF16)
         e = launch_gemm_f16(p, in[0], in[1], out, s.M, s.N, s.K, st);
       else
-        e = launch_gemm_generic(t.dtype, t.layout, in[0], in[1], out, s.M, s.N, s.K, st);
+        e = launch_gemm_generic(p.variant, t.dtype, t.layout, in[0], in[1], out, s.M, s.N, s.K, st);
       break;
     case OpKind::Conv:
       e = launch_conv_igemm(p, s, t.layout, static_cast<const float*>(in[0]), static_cast<const float*>(in[1]),

@@ -173,6 +173,8 @@ std::optional<Plan> solve_rows(const Hcs& h, const KmlTree& t, const Shape& s, S
 }
 
 // ---------------------------------------------------------------------------------------
+constexpr double kGemmF32Eff = 0.65;  // gemm_f32_kernel's fraction of the f32 MFMA rate (calibrated at 1024^3)
+
 std::optional<Plan> solve_gemm(const Hcs& h, const KmlTree& t, const Shape& s, SolveLog* log, std::string* err) {
   const double peak_tflops = t.dtype == DType::F16 ? (h.peak_f16_mfma_tflops > 0 ? h.peak_f16_mfma_tflops : h.flops_gflops * 1e-3)
                                                    : (h.peak_f32_mfma_tflops > 0 ? h.peak_f32_mfma_tflops : h.flops_gflops * 1e-3 / 16);
@@ -248,9 +250,32 @@ std::optional<Plan> solve_gemm(const Hcs& h, const KmlTree& t, const Shape& s, S
       cs.push_back(c);
     }
   }
+  if (t.dtype == DType::F32) {
+    const std::string key = "gemm_f32:64x64x64,w8";
+    if (!(s.M % 64 == 0 && s.N % 64 == 0 && s.K % 64 == 0)) {
+      reject(log, key + " violates M%64==0 && N%64==0 && K%64==0");
+    } else {
+      // One 64x64 tile per workgroup, eight wavefronts (two per SIMD, splitting each k-tile):
+      // the busiest CU's tiles at the calibrated fraction of its f32 MFMA rate.
+      const int64_t tiles = (s.M / 64) * (s.N / 64);
+      const double cu_flops_per_us = peak_tflops * 1e6 / double(cus(h));
+      const double per_cu = std::ceil(double(tiles) / cus(h));
+      Cand c;
+      c.plan.family = Family::GemmGeneric;
+      c.plan.variant = 1;
+      c.plan.tile_m = c.plan.tile_n = c.plan.tile_k = 64;
+      c.plan.threads = 512;
+      c.plan.grid = tiles;
+      c.plan.key = key;
+      c.plan.why = std::to_string(tiles) + " tiles of 64x64, LDS-staged k-tiles of 64 split over two wavefronts per SIMD";
+      c.cost = launch_us(h) + per_cu * 2.0 * 64 * 64 * double(s.K) / (cu_flops_per_us * kGemmF32Eff) + 1.0;
+      cs.push_back(c);
+    }
+  }
   {
     Cand c;
     c.plan.family = Family::GemmGeneric;
+    c.plan.variant = 0;
     c.plan.tile_m = c.plan.tile_n = kGemmGenericTile;
     c.plan.tile_k = 16;
     c.plan.threads = 256;

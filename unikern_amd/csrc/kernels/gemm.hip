@@ -35,9 +35,19 @@
 //   the accumulator bytes per flop of the 32x32x16 form; this chip runs the GEMM at its power
 //   limit, so the saving shows up as a higher sustained clock.
 //
+// gemm_f32_kernel — f32 C = A . B (B stored [K][N] or [N][K]) on v_mfma_f32_32x32x2f32 for
+//   M, N, K multiples of 64: a 64x64 tile per workgroup of eight wavefronts. Each k-tile of 64
+//   is staged in LDS (float4 loads and stores, rows padded to 68 floats so the fragment reads
+//   of eight lanes hit distinct bank groups) and split between two wavefronts per SIMD: waves
+//   0-3 multiply its first 32 k, waves 4-7 its last 32, each a 32x32 quarter of the tile, so one
+//   wavefront's LDS reads and waits overlap the other's MFMAs. A lane's float4 of A (and of B
+//   when B is [N][K]) feeds four MFMAs: MFMA (q, e) pairs k = 8q + e on lanes 0-31 with
+//   k = 8q + 4 + e on lanes 32-63 (any assignment of k to MFMA steps gives the same sum when A
+//   and B agree). The two halves' accumulators add in LDS in a fixed order.
+//
 // gemm_generic_kernel — any M, N, K, either B layout, f16 or f32 inputs: 64x64 tiles,
 //   bounds-checked element loads, MFMA 32x32x16 f16 or 32x32x2 f32. Used for shapes the
-//   fast kernel's divisibility predicates reject and for the f32 GEMM.
+//   fast kernels' divisibility predicates reject.
 #include "../launch.hpp"
 #include "../variants.hpp"
 #include "common.hpp"
@@ -446,6 +456,101 @@ __global__ void __launch_bounds__(512, 1)
 }
 
 // ---------------------------------------------------------------------------------------
+// f32 GEMM, 64x64x64 tiles, eight wavefronts (two k halves x 2x2 quarters).
+// ---------------------------------------------------------------------------------------
+constexpr int kF32Pitch = 68;  // floats per staged row (64 + 4 padding)
+
+template <bool BT>
+__global__ void __launch_bounds__(512)
+    gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N,
+                    int K) {
+  constexpr int kBuf = 2 * 64 * kF32Pitch;  // A and B of one k-tile
+  __shared__ __attribute__((aligned(16))) float lds[2 * kBuf];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kh = w >> 2, wm = (w >> 1) & 1, wn = w & 1;
+  const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+  // Staging: thread -> rows (tid >> 4) + 32u (u < 2), float4 column tid & 15 of a 64-float row:
+  // A rows are m, B rows are n (B [N][K]) or k (B [K][N]).
+  const int srow = tid >> 4, scol = (tid & 15) * 4;
+  const float* a_src = A + (int64_t)(m0 + srow) * K + scol;
+  const float* b_src = BT ? B + (int64_t)(n0 + srow) * K + scol : B + (int64_t)srow * N + n0 + scol;
+  const int64_t a_step32 = (int64_t)32 * K;                 // 32 rows of A
+  const int64_t b_step32 = BT ? (int64_t)32 * K : (int64_t)32 * N;
+  f32x4 ra[2], rb[2];
+  auto load = [&](int t) __attribute__((always_inline)) {
+    const int k0 = t * 64;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      ra[u] = *reinterpret_cast<const f32x4*>(a_src + u * a_step32 + k0);
+      rb[u] = BT ? *reinterpret_cast<const f32x4*>(b_src + u * b_step32 + k0)
+                 : *reinterpret_cast<const f32x4*>(b_src + u * b_step32 + (int64_t)k0 * N);
+    }
+  };
+  auto store = [&](int b) __attribute__((always_inline)) {
+    float* as = lds + b * kBuf;
+    float* bs = as + 64 * kF32Pitch;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      *reinterpret_cast<f32x4*>(as + (srow + 32 * u) * kF32Pitch + scol) = ra[u];
+      *reinterpret_cast<f32x4*>(bs + (srow + 32 * u) * kF32Pitch + scol) = rb[u];
+    }
+  };
+  const int fi = lane & 31, fh = lane >> 5;
+  const int kb = 32 * kh + 4 * fh;  // this lane's k offset within the tile (plus 8q + e)
+  f32x16 acc = f32x16{};
+  auto multiply = [&](int b) __attribute__((always_inline)) {
+    const float* as = lds + b * kBuf;
+    const float* bs = as + 64 * kF32Pitch;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const f32x4 av = *reinterpret_cast<const f32x4*>(as + (wm * 32 + fi) * kF32Pitch + kb + 8 * q);
+      f32x4 bv;
+      if constexpr (BT) {
+        bv = *reinterpret_cast<const f32x4*>(bs + (wn * 32 + fi) * kF32Pitch + kb + 8 * q);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bv[e] = bs[(kb + 8 * q + e) * kF32Pitch + wn * 32 + fi];
+      }
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, bv.x, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, bv.y, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, bv.z, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, bv.w, acc, 0, 0, 0);
+    }
+  };
+  const int KT = K / 64;
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int t = 0; t < KT; ++t) {
+    // The next tile's loads are in flight during this tile's MFMAs (the last pass repeats the
+    // last tile: unbranched, so the loads are not sunk behind the MFMAs).
+    load(t + 1 < KT ? t + 1 : t);
+    __builtin_amdgcn_sched_barrier(0);
+    multiply(t & 1);
+    __builtin_amdgcn_sched_barrier(0);
+    store((t + 1) & 1);  // its last readers (tile t - 1) passed the previous barrier
+    __syncthreads();
+  }
+  // D[i][j]: lane -> column j = lane & 31, rows i = 8 (r / 4) + 4 (lane >> 5) + r % 4. The k
+  // halves add in LDS (first half + second half) and the first half stores.
+  float* red = lds;  // every wavefront passed the last barrier: the ring is free
+  const int q4 = w & 3;
+  if (kh == 1) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[(q4 * 16 + r) * 64 + lane] = acc[r];
+  }
+  __syncthreads();
+  if (kh == 1) return;
+  const int j = n0 + wn * 32 + fi;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int i = m0 + wm * 32 + (r >> 2) * 8 + fh * 4 + (r & 3);
+    C[(int64_t)i * N + j] = acc[r] + red[(q4 * 16 + r) * 64 + lane];
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // Generic MFMA GEMM: 64x64 tile, 4 wavefronts (2x2 of 32x32), BK = 16, bounds-checked.
 // T = _Float16 or float inputs; TO = output type; BT: B stored [N][K] (TN) else [K][N] (NT).
 // ---------------------------------------------------------------------------------------
@@ -560,13 +665,28 @@ hipError_t launch_gemm_f16(const Plan& p, const void* A, const void* B, void* C,
   }
 }
 
-hipError_t launch_gemm_generic(DType dt, Layout lay, const void* A, const void* B, void* C, int64_t M, int64_t N,
-                               int64_t K, hipStream_t s) {
+bool gemm_f32_tiled_supported(int64_t M, int64_t N, int64_t K) {
+  return M > 0 && N > 0 && K > 0 && M % 64 == 0 && N % 64 == 0 && K % 64 == 0;
+}
+
+hipError_t launch_gemm_generic(int variant, DType dt, Layout lay, const void* A, const void* B, void* C, int64_t M,
+                               int64_t N, int64_t K, hipStream_t s) {
   if (M <= 0 || N <= 0 || K <= 0 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return hipErrorInvalidValue;
   if (lay != Layout::NT && lay != Layout::TN) return hipErrorInvalidValue;
   if ((M + 63) / 64 > 65535) return hipErrorInvalidValue;
   const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
   const bool bt = lay == Layout::TN;
+  if (variant == 1) {  // gemm_f32_kernel: f32, 64-multiples, 16-byte aligned operands
+    if (dt != DType::F32 || !gemm_f32_tiled_supported(M, N, K)) return hipErrorInvalidValue;
+    if ((((uintptr_t)A) | ((uintptr_t)B) | ((uintptr_t)C)) & 15) return hipErrorInvalidValue;
+    auto a = static_cast<const float*>(A);
+    auto b = static_cast<const float*>(B);
+    auto c = static_cast<float*>(C);
+    if (bt) hipLaunchKernelGGL((kern::gemm_f32_kernel<true>), grid, dim3(512), 0, s, a, b, c, (int)M, (int)N, (int)K);
+    else hipLaunchKernelGGL((kern::gemm_f32_kernel<false>), grid, dim3(512), 0, s, a, b, c, (int)M, (int)N, (int)K);
+    return hipGetLastError();
+  }
+  if (variant != 0) return hipErrorInvalidValue;
   if (dt == DType::F16) {
     auto a = static_cast<const _Float16*>(A);
     auto b = static_cast<const _Float16*>(B);

@@ -19,8 +19,10 @@ hipError_t launch_reduce1d(const float* X, float* partials, float* Y, int64_t n,
 
 hipError_t launch_gemm_f16(const Plan& p, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
                            hipStream_t s);
-hipError_t launch_gemm_generic(DType dt, Layout lay, const void* A, const void* B, void* C, int64_t M, int64_t N,
-                               int64_t K, hipStream_t s);
+// variant 0: gemm_generic_kernel (any shape); 1: gemm_f32_kernel (f32, M, N, K multiples of 64).
+hipError_t launch_gemm_generic(int variant, DType dt, Layout lay, const void* A, const void* B, void* C, int64_t M,
+                               int64_t N, int64_t K, hipStream_t s);
+bool gemm_f32_tiled_supported(int64_t M, int64_t N, int64_t K);
 hipError_t launch_q8_gemm(const Plan& p, const void* X, const void* Wq, float* Y, int64_t M, int64_t N, int64_t K,
                           hipStream_t s);
 hipError_t launch_conv_igemm(const Plan& p, const Shape& sh, Layout lay, const float* X, const float* Wt,
