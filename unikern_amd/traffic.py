@@ -29,6 +29,7 @@ KERNELS = {
     "softmax": re.compile(r"rows_kernel<\d+, \d+, 2[,>]"),
     "copy": re.compile(r"channelscale4_kernel"),
     "gemm_f16": re.compile(r"gemm_f16_(tn|pp)_kernel"),
+    "gemm_f32": re.compile(r"gemm_f32_kernel"),
     "gemm_generic": re.compile(r"gemm_generic_kernel"),
     "conv": re.compile(r"conv_igemm_kernel|conv_tile_kernel|conv_lds_kernel"),
     "q8_0": re.compile(r"q8_0_gemm_kernel"),
