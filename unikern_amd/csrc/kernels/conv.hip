@@ -413,8 +413,13 @@ __global__ void __launch_bounds__(256 * PT)
   const int oh = wave & 1, ph = wave >> 1;  // output-channel half, 32-pixel group
   const int P = a.Ho * a.Wo;
   const int tiles = (P + kPix - 1) / kPix;
-  const int n = blockIdx.x / tiles;
-  const int p0 = (blockIdx.x - n * tiles) * kPix;
+  // XCD-aware order: workgroup b runs on XCD b % 8, so XCD x takes a contiguous run of tiles
+  // (runs of G / 8 or G / 8 + 1) and neighbouring tiles' shared input rows hit its L2.
+  const int G = gridDim.x, q8 = G >> 3, r8 = G & 7;
+  const int xcd = blockIdx.x & 7;
+  const int lin = xcd * q8 + (xcd < r8 ? xcd : r8) + (blockIdx.x >> 3);
+  const int n = lin / tiles;
+  const int p0 = (lin - n * tiles) * kPix;
   const int r0 = p0 / a.Wo;
   const int rlast = ((p0 + kPix - 1 < P) ? p0 + kPix - 1 : P - 1) / a.Wo;
   const int in_rows = rlast - r0 + 3;  // padded input rows r0 .. rlast + 2
