@@ -403,6 +403,10 @@ constexpr int kXlFloats = 2 * kLdsRows * kLdsCols * 4;         // 4096 floats = 
 constexpr int kWlFloats = 64 * kWPitch;                        // 4864 floats = 19 KiB
 constexpr int kConvLdsBuf = kXlFloats + kWlFloats;
 
+// PT = 2: taps multiplied before the next chunk (loaded two chunks ahead, so landed) is written
+// to LDS; the rest of the chunk's MFMAs follow the writes (3, 5 and 7 measured within 1%).
+constexpr int kMidTap = 5;
+
 template <int PT>
 __global__ void __launch_bounds__(256 * PT)
     conv_lds_kernel(ConvArgs a) {
@@ -528,9 +532,9 @@ __global__ void __launch_bounds__(256 * PT)
   const int wbase = kXlFloats + (oh * 32 + (lane & 31)) * kWPitch + 4 * kk;
 
   f32x16 acc[4] = {f32x16{}, f32x16{}, f32x16{}, f32x16{}};
-  auto multiply = [&](const float* cur) __attribute__((always_inline)) {
+  auto multiply = [&](const float* cur, int t0, int t1) __attribute__((always_inline)) {
 #pragma unroll
-    for (int t = 0; t < 9; ++t) {
+    for (int t = t0; t < t1; ++t) {
       const int kh = t / 3, kw = t % 3;
       const f32x4 xv = *reinterpret_cast<const f32x4*>(cur + xbase + (kh * kLdsCols + kw) * 4);
       const f32x4 wv = *reinterpret_cast<const f32x4*>(cur + wbase + t * 8);
@@ -557,19 +561,20 @@ __global__ void __launch_bounds__(256 * PT)
   // store under a branch lets the compiler sink loads behind the MFMAs, or makes its wait
   // counting (which cannot tell that a skipped step also leaves the loop) wait for loads that
   // should stay in flight. The other buffer's last readers (chunk k - 1) all passed the previous
-  // barrier when chunk k + 1 is written to it. (Writing it halfway through the taps instead
-  // measured slower.)
+  // barrier when chunk k + 1 is written to it.
   if constexpr (PT == 2) {
     // Two chunks ahead: chunk k's `mine` set (already in LDS) takes chunk k + 2's loads and
-    // `next` (chunk k + 1) is written after chunk k's MFMAs. The input streams from HBM and one
-    // chunk's MFMAs do not cover its load latency. With an odd chunk count the last step
-    // (k = chunks) only repeats loads and a store.
+    // `next` (chunk k + 1, loaded during chunk k - 1) is written between chunk k's MFMAs. The
+    // input streams from HBM and one chunk's MFMAs do not cover its load latency. With an odd
+    // chunk count the last step (k = chunks) only repeats loads and a store.
     auto step = [&](int k, Stage& mine, const Stage& next) __attribute__((always_inline)) {
       load_chunk(mine, 8 * (k + 2 < chunks ? k + 2 : chunks - 1));
       __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the MFMAs
-      if (k < chunks) multiply(lds + (k & 1) * kConvLdsBuf);
+      if (k < chunks) multiply(lds + (k & 1) * kConvLdsBuf, 0, kMidTap);
       __builtin_amdgcn_sched_barrier(0);  // no use of the loaded registers ahead of the MFMAs
       store_chunk(next, (k + 1) & 1);
+      __builtin_amdgcn_sched_barrier(0);
+      if (k < chunks) multiply(lds + (k & 1) * kConvLdsBuf, kMidTap, 9);
       if (k + 1 < chunks) __syncthreads();
     };
     for (int k = 0; k < chunks; k += 2) {
@@ -577,11 +582,13 @@ __global__ void __launch_bounds__(256 * PT)
       step(k + 1, sb, sa);
     }
   } else {
-    // One chunk ahead (a second register set would cost the second workgroup per CU).
+    // One chunk ahead (a second register set would cost the second workgroup per CU); the
+    // store follows all of the chunk's MFMAs (writing it halfway through, before its loads have
+    // had a whole chunk to land, measured slower).
     for (int k = 0; k < chunks; ++k) {
       load_chunk(sa, 8 * (k + 1 < chunks ? k + 1 : k));
       __builtin_amdgcn_sched_barrier(0);
-      multiply(lds + (k & 1) * kConvLdsBuf);
+      multiply(lds + (k & 1) * kConvLdsBuf, 0, 9);
       __builtin_amdgcn_sched_barrier(0);
       store_chunk(sa, (k + 1) & 1);
       if (k + 1 < chunks) __syncthreads();
