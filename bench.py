@@ -419,7 +419,8 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the kernels shard without exchange, see DESIGN.md)", file=sys.stderr)
+              "(every kernel family would shard by rows, tiles or batch without exchange; "
+              "no multi-GPU run is part of this build)", file=sys.stderr)
         sys.exit(2)
 
     import _oracle as O
