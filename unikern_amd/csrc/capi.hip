@@ -926,17 +926,36 @@ int uk_run(const char* hcs_json, const uk_op_desc* d, const uk_plan* plan, uint6
   out->tol_kind = rd.tol_kind;
 
   // Kernel-only timing: warm-up, then `repeats` x `iters` back-to-back launches over the
-  // rotating sets; per-launch time is the median over repeats.
+  // rotating sets; per-launch time is the median over repeats. The warm-up runs for at least
+  // kSettleMs of device time: the part raises its clocks over several milliseconds of load, and
+  // a kernel timed right after an idle gap runs 10-20% slow at first.
+  constexpr double kSettleMs = 50.0;
+  constexpr int kMaxSettleLaunches = 100000;
   const int iters = timing_iters > 0 ? timing_iters : 50;
   const int repeats = 5;
   const int warm = std::max(20, n_sets);
   int li = 0;
-  for (int i = 0; i < warm; ++i, ++li) {
-    const int sset = li % n_sets;
-    if (int rc = dispatch(t, p, const_cast<const void* const*>(&ins[size_t(sset) * n_in]), outs[sset], st))
-      return finish(rc);
+  auto launches = [&](int n) -> int {
+    for (int i = 0; i < n; ++i, ++li) {
+      const int sset = li % n_sets;
+      if (int rc = dispatch(t, p, const_cast<const void* const*>(&ins[size_t(sset) * n_in]), outs[sset], st)) return rc;
+    }
+    return 0;
+  };
+  if ((he = hipEventRecord(e0, st)) != hipSuccess) return hip_fail(he, "record");
+  if (int rc = launches(warm)) return finish(rc);
+  if ((he = hipEventRecord(e1, st)) != hipSuccess) return hip_fail(he, "record");
+  if ((he = hipEventSynchronize(e1)) != hipSuccess) return hip_fail(he, "sync warm");
+  {
+    float warm_ms = 0;
+    if ((he = hipEventElapsedTime(&warm_ms, e0, e1)) != hipSuccess) return hip_fail(he, "elapsed");
+    const double per = double(warm_ms) / warm;
+    if (per > 0 && warm_ms < kSettleMs) {
+      const int extra = int(std::min<double>(kMaxSettleLaunches, (kSettleMs - warm_ms) / per));
+      if (int rc = launches(extra)) return finish(rc);
+      if ((he = hipStreamSynchronize(st)) != hipSuccess) return hip_fail(he, "sync settle");
+    }
   }
-  if ((he = hipStreamSynchronize(st)) != hipSuccess) return hip_fail(he, "sync warm");
   std::vector<double> per;
   for (int r = 0; r < repeats; ++r) {
     if ((he = hipEventRecord(e0, st)) != hipSuccess) return hip_fail(he, "record");
