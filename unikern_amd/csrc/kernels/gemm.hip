@@ -310,8 +310,11 @@ constexpr int pp_lds_bytes() { return STAGES * kPpStage > kPpEpi ? STAGES * kPpS
 
 // Workgroup barrier without the memory fence __syncthreads() implies: the fence would make every
 // barrier wait for all outstanding copies, and each wait this kernel needs is issued explicitly.
-__device__ __forceinline__ void barrier_nofence() { __asm__ volatile("s_barrier" ::: "memory"); }
-__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4)); }
+__device__ __forceinline__ void barrier_nofence() {
+  __builtin_amdgcn_sched_barrier(0);
+  __asm__ volatile("s_barrier" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);  // nothing (an MFMA included) moves across the barrier
+}
 
 // Wait until at most 4 * n copies of this wavefront are outstanding (n = 0..3).
 __device__ __forceinline__ void wait_copies(int n) {
@@ -409,7 +412,8 @@ __global__ void __launch_bounds__(512, 1)
     for (int t = 0; t < KT; ++t) {
       read_frags(t);  // phase 2t
       if (t + STAGES - 1 < KT) issue(t + STAGES - 1);
-      wait_lgkm0();
+      // No wait for the fragment reads here: slot t is refilled only after b_{2t+2S-2}, which
+      // follows this group's MFMAs (and so its reads); the MFMAs wait for their fragments.
       barrier_nofence();  // b_{2t+1}
       multiply();  // phase 2t+1
       wait_copies(after(t));
@@ -420,7 +424,6 @@ __global__ void __launch_bounds__(512, 1)
     for (int t = 0; t < KT; ++t) {
       read_frags(t);  // phase 2t+1
       if (t + STAGES - 1 < KT) issue(t + STAGES - 1);
-      wait_lgkm0();
       wait_copies(after(t));
       barrier_nofence();  // b_{2t+2}
       multiply();  // phase 2t+2
