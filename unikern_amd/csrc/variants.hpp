@@ -34,13 +34,13 @@ constexpr RowsVariant kRowsVariants[] = {
     {1024, 1, 0, 1, 0.549, 0.585, 0.672},
     {1024, 2, 0, 1, 0.552, 0.583, 0.639},
     {1024, 4, 0, 1, 0.544, 0.597, 0.526},
-    {256, 4, 1, 1, 0.754, 0.696, 0.718},
-    {512, 2, 1, 1, 0.762, 0.704, 0.735},
+    {256, 4, 1, 1, 0.754, 0.717, 0.718},
+    {512, 2, 1, 1, 0.762, 0.713, 0.735},
     {1024, 1, 1, 1, 0.558, 0.598, 0.683},
     {512, 4, 1, 1, 0.759, 0.702, 0.717},
     {1024, 2, 1, 1, 0.562, 0.606, 0.642},
     {128, 8, 1, 1, 0.740, 0.704, 0.709},
-    {256, 4, 1, 2, 0.731, 0.714, 0.698},
+    {256, 4, 1, 2, 0.731, 0.718, 0.698},
     {512, 2, 1, 2, 0.742, 0.700, 0.681},
 };
 constexpr int kNumRowsVariants = sizeof(kRowsVariants) / sizeof(kRowsVariants[0]);
