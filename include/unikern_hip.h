@@ -107,6 +107,20 @@ int uk_abi_version(void);
 int uk_device_check(char* arch, size_t cap);
 /* Measured device facts: compute units, max LDS per workgroup, clock (kHz), total bytes. */
 int uk_device_props(int32_t* cus, int32_t* lds_per_block, int32_t* clock_khz, uint64_t* total_bytes);
+/* Matrix-core ceiling of the device, measured (the reference's calibrate derives HCS constants
+ * from measurements, src/solver.cpp:194-244; it has no matrix-core probe): one wavefront per
+ * SIMD issues only independent v_mfma_f32_32x32x16_f16 for a few milliseconds after at least
+ * 50 ms of the same load. tflops: sustained f16 MFMA rate; clock_ghz: shader clock over the loop
+ * (s_memtime against the 100 MHz s_memrealtime); cycles_per_mfma: issue interval per wavefront. */
+typedef struct uk_mfma_probe {
+  double tflops;
+  double clock_ghz;
+  double cycles_per_mfma;
+  double ms_per_launch;
+  int32_t workgroups;
+  int32_t mfmas_per_wave;
+} uk_mfma_probe;
+int uk_probe_mfma(uk_mfma_probe* out);
 const char* uk_last_error(void);
 
 /* ---- KML op specs (reference src/kml_front.cpp:203-251, src/kml.cpp:57-177) ---- */

@@ -22,7 +22,7 @@ import numpy as np
 
 from . import _capi
 from ._capi import (DTYPES, FAMILIES, LAYOUTS, OPS, UK_BAD_INVOCATION, UK_HIP_FAILURE, UK_INFEASIBLE, UK_OK,
-                    UK_RESIDENCY, UK_VERIFY_FAIL, OpDesc, Plan, Result)
+                    UK_RESIDENCY, UK_VERIFY_FAIL, MfmaProbe, OpDesc, Plan, Result)
 
 lib = _capi.load()
 CLI = Path(__file__).resolve().parent / "unikern"  # the command-line front door (built with the library)
@@ -227,6 +227,17 @@ def device_props() -> dict:
         raise UnikernError(rc, last_error())
     return {"compute_units": cus.value, "lds_per_block": lds.value, "clock_khz": clk.value,
             "total_bytes": tot.value}
+
+
+def probe_mfma() -> dict:
+    """Matrix-core ceiling of the device (uk_probe_mfma): sustained f16 MFMA TFLOP/s, the shader
+    clock under that load and the issue cycles per v_mfma_f32_32x32x16_f16."""
+    r = MfmaProbe()
+    rc = lib.uk_probe_mfma(C.byref(r))
+    if rc != UK_OK:
+        raise UnikernError(rc, last_error())
+    return {"tflops": r.tflops, "clock_ghz": r.clock_ghz, "cycles_per_mfma": r.cycles_per_mfma,
+            "ms_per_launch": r.ms_per_launch, "workgroups": r.workgroups, "mfmas_per_wave": r.mfmas_per_wave}
 
 
 def _check(rc: int):

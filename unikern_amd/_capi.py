@@ -42,11 +42,17 @@ class Result(C.Structure):
                 ("mode", C.c_char * 16), ("dtype", C.c_char * 8), ("perf", C.c_char * 48)]
 
 
+class MfmaProbe(C.Structure):
+    _fields_ = [("tflops", C.c_double), ("clock_ghz", C.c_double), ("cycles_per_mfma", C.c_double),
+                ("ms_per_launch", C.c_double), ("workgroups", C.c_int32), ("mfmas_per_wave", C.c_int32)]
+
+
 _P = C.c_void_p
 _SIG = {
     "uk_abi_version": ([], C.c_int),
     "uk_device_check": ([C.c_char_p, C.c_size_t], C.c_int),
     "uk_device_props": ([C.POINTER(C.c_int32)] * 3 + [C.POINTER(C.c_uint64)], C.c_int),
+    "uk_probe_mfma": ([C.POINTER(MfmaProbe)], C.c_int),
     "uk_last_error": ([], C.c_char_p),
     "uk_kml_import": ([C.c_char_p, C.POINTER(OpDesc), C.c_char_p, C.c_size_t], C.c_int),
     "uk_kml_export": ([C.c_char_p, C.c_char_p, C.c_size_t], C.c_int),

@@ -638,6 +638,71 @@ int uk_device_props(int32_t* cus, int32_t* lds_per_block, int32_t* clock_khz, ui
   return UK_OK;
 }
 
+int uk_probe_mfma(uk_mfma_probe* out) {
+  if (!out) return fail(UK_BAD_INVOCATION, "null argument");
+  int dev = 0;
+  hipDeviceProp_t prop{};
+  if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess)
+    return fail(UK_HIP_FAILURE, "UNIKERN_ERROR what=hipGetDeviceProperties");
+  // One workgroup of four wavefronts per CU (one per SIMD); kProbeChains x 16384 MFMAs per
+  // wavefront, about 2 ms per launch.
+  const int wgs = prop.multiProcessorCount;
+  constexpr int kIters = 16384;
+  constexpr double kSettleMs = 50.0;
+  constexpr int kTimed = 5;
+  const size_t words = size_t(wgs) * 4 * 3;
+  unsigned long long* d = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  auto done = [&](int rc) {
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (d) (void)hipFree(d);
+    return rc;
+  };
+  auto hip_fail = [&](hipError_t e, const char* what) {
+    return fail(UK_HIP_FAILURE, std::string("UNIKERN_ERROR what=") + what + " msg=" + hipGetErrorString(e));
+  };
+  hipError_t he;
+  if ((he = hipMalloc(&d, words * sizeof(unsigned long long))) != hipSuccess) return done(hip_fail(he, "hipMalloc"));
+  if ((he = hipEventCreate(&e0)) != hipSuccess || (he = hipEventCreate(&e1)) != hipSuccess)
+    return done(hip_fail(he, "hipEventCreate"));
+  // Settle the clocks under this load, then time kTimed back-to-back launches.
+  float ms = 0;
+  double settled = 0;
+  while (settled < kSettleMs) {
+    if ((he = hipEventRecord(e0, nullptr)) != hipSuccess) return done(hip_fail(he, "record"));
+    if ((he = launch_mfma_probe(wgs, kIters, d, nullptr)) != hipSuccess) return done(hip_fail(he, "probe launch"));
+    if ((he = hipEventRecord(e1, nullptr)) != hipSuccess) return done(hip_fail(he, "record"));
+    if ((he = hipEventSynchronize(e1)) != hipSuccess) return done(hip_fail(he, "sync"));
+    if ((he = hipEventElapsedTime(&ms, e0, e1)) != hipSuccess) return done(hip_fail(he, "elapsed"));
+    if (ms <= 0) return done(fail(UK_HIP_FAILURE, "UNIKERN_ERROR what=probe_timing"));
+    settled += ms;
+  }
+  if ((he = hipEventRecord(e0, nullptr)) != hipSuccess) return done(hip_fail(he, "record"));
+  for (int i = 0; i < kTimed; ++i)
+    if ((he = launch_mfma_probe(wgs, kIters, d, nullptr)) != hipSuccess) return done(hip_fail(he, "probe launch"));
+  if ((he = hipEventRecord(e1, nullptr)) != hipSuccess) return done(hip_fail(he, "record"));
+  if ((he = hipEventSynchronize(e1)) != hipSuccess) return done(hip_fail(he, "sync"));
+  if ((he = hipEventElapsedTime(&ms, e0, e1)) != hipSuccess) return done(hip_fail(he, "elapsed"));
+  std::vector<unsigned long long> h(words);
+  if ((he = hipMemcpy(h.data(), d, words * sizeof(unsigned long long), hipMemcpyDeviceToHost)) != hipSuccess)
+    return done(hip_fail(he, "copy"));
+  double cycles = 0, ticks = 0;
+  for (size_t w = 0; w < words / 3; ++w) {
+    cycles += double(h[3 * w]);
+    ticks += double(h[3 * w + 1]);
+  }
+  const double mfmas = double(kIters) * kProbeChains;
+  const double per_launch_ms = double(ms) / kTimed;
+  out->workgroups = wgs;
+  out->mfmas_per_wave = int32_t(mfmas);
+  out->ms_per_launch = per_launch_ms;
+  out->tflops = double(wgs) * 4 * mfmas * 32768.0 / (per_launch_ms * 1e-3) / 1e12;
+  out->clock_ghz = ticks > 0 ? cycles / ticks * 0.1 : 0;  // ticks at 100 MHz
+  out->cycles_per_mfma = cycles / (double(words / 3) * mfmas);
+  return done(UK_OK);
+}
+
 int uk_kml_import(const char* json, uk_op_desc* out, char* err, size_t cap) {
   if (!json || !out) return fail(UK_BAD_INVOCATION, "null argument");
   std::string e;
