@@ -289,7 +289,7 @@ std::optional<Plan> solve_gemm(const Hcs& h, const KmlTree& t, const Shape& s, S
 }
 
 // ---------------------------------------------------------------------------------------
-constexpr double kActBytesPerUsPerCu = 74e3;  // activation bytes per us per CU and round (fitted)
+constexpr double kActBytesPerUsPerCu = 100e3;  // activation bytes per us per CU (fitted)
 
 std::optional<Plan> solve_q8(const Hcs& h, const KmlTree& t, const Shape& s, SolveLog* log, std::string* err) {
   const Workload w = workload_of(t);
@@ -314,28 +314,32 @@ std::optional<Plan> solve_q8(const Hcs& h, const KmlTree& t, const Shape& s, Sol
     // Pairs of the last round beyond K/64 are copied and skipped: wasted bandwidth.
     const double useful = double(npairs) / double(rounds * per_round);
     const int64_t grid = ((s.N + 16 * v.nt - 1) / (16 * v.nt)) * ((s.M + 15) / 16);
-    const int wps = waves_by_regs(h, 96);
+    // VGPRs per lane: activation fragments (8 per pair, twice with double buffering) and the
+    // accumulators of each weight tile on a fixed base (the compiled variants use 70-133).
+    const int regs = 40 + 10 * v.pairs * (v.db ? 2 : 1) + 16 * (v.nt - 1);
+    const int wps = waves_by_regs(h, regs);
     const int resident = std::max(1, std::min<int>(wps * simds(h) / v.waves, int(lds_cu(h) / lds)));
     // Bytes in flight per workgroup: one round of copies (two with double buffering).
     const double inflight = double(per_round) * 16.0 * v.nt * 68.0 * useful * (v.db && rounds > 1 ? 2.0 : 1.0);
     // Copy instructions: 16-byte copies issue a quarter of the dword ones.
-    const double issue_us = double(rounds) * (v.vec == 4 ? 0.3 : 1.2);
+    const double issue_us = double(rounds) * (v.vec == 4 ? 0.1 : 0.4);
     // Each generation of resident workgroups waits one load latency before its first round
-    // lands and folds its split-K partials after its last; nothing overlaps those within a
-    // generation (fitted: about 1 us per generation over the variants at N = 11008).
+    // lands and folds its split-K partials after its last.
     const int64_t slots = int64_t(cus(h)) * resident;
     const int64_t generations = (grid + slots - 1) / slots;
-    const double gen_us = double(generations) * 0.5 * kMemLatencyUs;
+    const double gen_us = double(generations) * 0.25 * kMemLatencyUs;
     // Every workgroup reads its activation rows over all of K (from L2); the n-tiles of a
-    // workgroup share each activation fragment. Fitted over the variants at the BASELINE shapes:
-    // the busiest CU's activation bytes cost about 1 us per 74 KB for each round of a wavefront
-    // (a round's wait covers its activation loads with its copies), and without double
-    // buffering every round after the first exposes half a load latency.
+    // workgroup share each activation fragment: the busiest CU's activation bytes.
     const double act_cu = std::ceil(double(grid) / cus(h)) * double(std::min<int64_t>(s.M, 16)) * double(s.K) * 2.0;
-    const double act_us = act_cu * double(rounds) / kActBytesPerUsPerCu;
-    const double rounds_us = v.db ? 0.0 : double(rounds - 1) * 0.5 * kMemLatencyUs;
+    const double act_us = act_cu / kActBytesPerUsPerCu;
+    // Without double buffering a round's compute and the next round's load latency are serial
+    // within a wavefront; the other resident wavefronts of the CU hide that (fitted over the
+    // variants at the BASELINE shapes: half a latency at 16 resident wavefronts per CU).
+    const double rounds_us = v.db ? 0.0 : double(rounds - 1) * 0.1 * kMemLatencyUs;
+    const int64_t waves_cu = std::min<int64_t>(resident, (grid + cus(h) - 1) / cus(h)) * v.waves;
+    const double hide_us = 0.5 * kMemLatencyUs * 16.0 / double(std::max<int64_t>(waves_cu, 1));
     const double cost = launch_us(h) + stream_us(h, double(w.bytes) / useful, grid, resident, inflight) + issue_us +
-                        gen_us + act_us + rounds_us;
+                        gen_us + act_us + rounds_us + hide_us;
     Cand c;
     c.plan.family = Family::Q8Gemm;
     c.plan.variant = i;

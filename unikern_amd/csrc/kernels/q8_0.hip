@@ -32,7 +32,8 @@
 // covers WAVES * P pairs; wavefront w takes pairs [w * P, w * P + P) of it. Each wavefront
 // accumulates in registers across rounds; the partials fold in LDS in wavefront order
 // (deterministic). Weight rows past N read row n0 (valid memory) and are never stored;
-// activation rows past M read as zero; pairs past K/64 are copied from pair 0 and skipped.
+// activation rows past M read row 0 and feed only output rows past M, which are never stored;
+// pairs past K/64 are copied from pair 0 and skipped.
 #include "../launch.hpp"
 #include "../variants.hpp"
 #include "common.hpp"
@@ -143,8 +144,10 @@ __global__ void __launch_bounds__(WAVES * 64)
     for (int j = 0; j < P; ++j) {
       const int p = p0 + j;
       if (p >= npairs) break;  // wave-uniform: the last round's tail
-      const f16x8 x0 = mok ? xa[j] : f16x8{};
-      const f16x8 x1 = mok ? xb[j] : f16x8{};
+      // Lanes of activation rows past M hold row 0's values (finite): they only feed output
+      // rows past M, which are never stored, so no select is spent on them.
+      const f16x8 x0 = xa[j];
+      const f16x8 x1 = xb[j];
       // The pair's activations serve the NT 16-row tiles of weights.
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
@@ -272,6 +275,7 @@ hipError_t launch_q8_gemm(const Plan& p, const void* X, const void* Wq, float* Y
   UK_Q8_CASE(4, 4, 4, 1, 1)
   UK_Q8_CASE(4, 8, 4, 1, 1)
   UK_Q8_CASE(8, 4, 4, 0, 4)
+  UK_Q8_CASE(8, 4, 4, 0, 1)
 #undef UK_Q8_CASE
   return hipErrorInvalidValue;
 }
