@@ -141,3 +141,18 @@ def test_calibrated_gemm_pick(uk):
     s = uk.solve(uk.make_desc("gemm", [4096, 4096, 4096], dtype="fp16", layout="TN"))
     assert s.key == "gemm_f16:256x256x32,w2x4,s4,z2,pp"
     assert s.plan.tile_m == 256 and s.plan.threads == 512
+
+
+@pytest.mark.parametrize("op,dims,kw", [("gemm", [4096, 4096, 4096], dict(dtype="fp16", layout="TN")),
+                                        ("conv", [56, 56, 64, 3, 3, 64],
+                                         dict(layout="NCHW", batch=8, pad=1, epilogue="channelscale")),
+                                        ("gemm", [8, 11008, 4096], dict(dtype="q8_0", layout="TN"))])
+def test_candidate_log_names_family_and_variant(uk, op, dims, kw):
+    # every feasible candidate is listed once, cheapest first, with the family and variant that
+    # run it: the first line is the pick itself
+    from unikern_amd.sweep import _CAND
+    s = uk.solve(uk.make_desc(op, dims, **kw))
+    c = _CAND.findall(s.log)
+    assert len(c) == s.feasible == len({(f, v) for _, f, v, _ in c})
+    assert c[0][0] == s.key and int(c[0][1]) == s.plan.family and int(c[0][2]) == s.plan.variant
+    assert [float(x[3]) for x in c] == sorted(float(x[3]) for x in c)

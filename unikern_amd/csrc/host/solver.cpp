@@ -98,7 +98,9 @@ std::optional<Plan> pick(std::vector<Cand>& cs, const char* family_name, SolveLo
   for (const Cand& c : cs)
     if (c.cost < best->cost || (c.cost == best->cost && c.plan.key < best->plan.key)) best = &c;
   if (log) {
-    for (const Cand& c : cs) log->ranked.emplace_back(c.cost, c.plan.key);
+    for (const Cand& c : cs)
+      log->ranked.emplace_back(c.cost, std::string(c.plan.key) + " family=" + std::to_string(int(c.plan.family)) +
+                                           " variant=" + std::to_string(c.plan.variant));
     std::sort(log->ranked.begin(), log->ranked.end());
   }
   Plan p = best->plan;

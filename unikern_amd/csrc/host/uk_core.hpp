@@ -165,7 +165,7 @@ struct Plan {
 
 struct SolveLog {
   std::vector<std::string> rejected;                // violated predicates (sample)
-  std::vector<std::pair<double, std::string>> ranked;  // feasible candidates by predicted us
+  std::vector<std::pair<double, std::string>> ranked;  // feasible candidates ("key family=F variant=N") by predicted us
 };
 std::optional<Plan> solve(const Hcs& h, const KmlTree& t, SolveLog* log, std::string* err);
 
