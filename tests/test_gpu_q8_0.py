@@ -86,7 +86,7 @@ def test_ragged_shapes(gpu, M, N, K):
     assert frob(q8_gpu(gpu, Xh, blocks, N), O.q8_0_gemm(Xh, blocks, N)) <= 1e-5
 
 
-@pytest.mark.parametrize("vi", range(9))
+@pytest.mark.parametrize("vi", range(10))
 @pytest.mark.parametrize("K", [2048, 4608])
 def test_every_variant(gpu, vi, K):
     # K = 4608 (72 block pairs) leaves a partial last round for every variant; N = 300 leaves a

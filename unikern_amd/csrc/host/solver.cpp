@@ -341,10 +341,15 @@ std::optional<Plan> solve_q8(const Hcs& h, const KmlTree& t, const Shape& s, Sol
     // within a wavefront; the other resident wavefronts of the CU hide that (fitted over the
     // variants at the BASELINE shapes: half a latency at 16 resident wavefronts per CU).
     const double rounds_us = v.db ? 0.0 : double(rounds - 1) * 0.1 * kMemLatencyUs;
-    const int64_t waves_cu = std::min<int64_t>(resident, (grid + cus(h) - 1) / cus(h)) * v.waves;
+    // (A wavefront with nt weight tiles carries nt tiles' copies and compute: it counts nt times.)
+    const int64_t waves_cu = std::min<int64_t>(resident, (grid + cus(h) - 1) / cus(h)) * v.waves * v.nt;
     const double hide_us = 0.5 * kMemLatencyUs * 16.0 / double(std::max<int64_t>(waves_cu, 1));
-    const double cost = launch_us(h) + stream_us(h, double(w.bytes) / useful, grid, resident, inflight) + issue_us +
-                        gen_us + act_us + rounds_us + hide_us;
+    // A grid narrower than the chip streams through fewer CUs, each of which sustains about 1.25x
+    // its share of the peak (fitted: 64-row workgroups at N = 11008 leave 84 CUs idle).
+    const double cu_share = hbm_gbps(h) * 1e3 * kStreamEff / double(cus(h)) * 1.25;  // bytes per us
+    const double narrow_us = double(w.bytes) / useful / (double(std::min<int64_t>(grid, cus(h))) * cu_share);
+    const double stream = std::max(stream_us(h, double(w.bytes) / useful, grid, resident, inflight), narrow_us);
+    const double cost = launch_us(h) + stream + issue_us + gen_us + act_us + rounds_us + hide_us;
     Cand c;
     c.plan.family = Family::Q8Gemm;
     c.plan.variant = i;

@@ -276,6 +276,7 @@ hipError_t launch_q8_gemm(const Plan& p, const void* X, const void* Wq, float* Y
   UK_Q8_CASE(4, 8, 4, 1, 1)
   UK_Q8_CASE(8, 4, 4, 0, 4)
   UK_Q8_CASE(8, 4, 4, 0, 1)
+  UK_Q8_CASE(8, 4, 4, 0, 3)
 #undef UK_Q8_CASE
   return hipErrorInvalidValue;
 }

@@ -93,7 +93,7 @@ struct Q8Variant {
 };
 constexpr Q8Variant kQ8Variants[] = {{16, 4, 4, 0, 1}, {16, 4, 1, 0, 1}, {8, 8, 4, 0, 1}, {8, 4, 1, 0, 1},
                                      {8, 4, 4, 1, 1},  {4, 4, 4, 1, 1},  {4, 8, 4, 1, 1}, {8, 4, 4, 0, 4},
-                                     {8, 4, 4, 0, 1}};
+                                     {8, 4, 4, 0, 1},  {8, 4, 4, 0, 3}};
 constexpr int kNumQ8Variants = sizeof(kQ8Variants) / sizeof(kQ8Variants[0]);
 
 // Implicit-GEMM conv on f32 MFMA (v_mfma_f32_32x32x2f32). Wide kernel (tile_strips 0): a
