@@ -135,6 +135,9 @@ int uk_support_gap(const uk_op_desc* d, char* reason, size_t cap); /* 0 covered,
 /* ---- hardware description + solver (reference src/hcs.cpp, src/solver.cpp:141-186) ---- */
 int uk_hcs_fingerprint(const char* hcs_json, char* out, size_t cap); /* NULL json: built-in MI355X */
 int uk_hcs_export(const char* hcs_json, char* out, size_t cap);
+/* log: the SOLVE line, one "  rejected KEY violates ..." line per candidate a predicate
+   dropped, then one "  candidate KEY family=F variant=V predicted_us=T" line per feasible
+   candidate, cheapest first (a plan with that family and variant runs it). */
 int uk_solve(const char* hcs_json, const uk_op_desc* d, uk_plan* out, char* log, size_t cap);
 
 /* ---- execution ----
