@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define UK_ABI_VERSION 2
+#define UK_ABI_VERSION 3
 
 enum uk_status {
   UK_OK = 0,
@@ -102,6 +102,13 @@ typedef struct uk_result {
   char mode[16];
   char dtype[8];
   char perf[48];
+  /* The host side of the run, the SURVEY's cpu_ms=/cpu_cores= tokens: wall time of uk_run's
+   * own CPU reference pass (binary64, over the outputs it checks) on the inputs the device saw,
+   * the host threads that pass ran on, and how many outputs it computed (all of them, or the
+   * sampled rows/images of a GEMM or conv). -1 when not reported (a parsed line without them). */
+  double cpu_ms;
+  int32_t cpu_cores;
+  int64_t cpu_outputs;
 } uk_result;
 
 /* ---- library / device ---- */
@@ -161,8 +168,10 @@ int uk_solve(const char* hcs_json, const uk_op_desc* d, uk_plan* out, char* log,
  *   channelscale:  in[0]=X, in[1]=S[C]; out=Y
  * plan may be NULL (solved against the built-in MI355X description).
  * The 1-D reduce keeps its pass-1 partials in a library-owned buffer, one per (device, stream),
- * allocated on the first 1-D reduce enqueued on that stream and kept until the process ends;
- * launches on one stream run in order, so they never share partials with another stream. */
+ * allocated on the first 1-D reduce enqueued on that stream (8 KiB); launches on one stream run
+ * in order, so they never share partials with another stream. uk_stream_destroy frees its
+ * stream's buffer; a stream created outside the library keeps its buffer until the process ends
+ * (uk_launch_noalloc needs none). */
 int uk_launch(const uk_op_desc* d, const uk_plan* plan, const void* const* in, int32_t n_in, void* out,
               void* stream);
 /* uk_launch that allocates nothing: no counterpart in the reference; for callers that cannot
@@ -233,9 +242,11 @@ int uk_ledger_key(const char* hcs_json, const char* kml_json, char* out, size_t 
 /* *hit = 1 and the recorded plan (family, variant, key, tiles; predicted_us = c_ms * 1e3) on a hit. */
 int uk_ledger_lookup(void* ledger, const char* hcs_json, const char* kml_json, uk_plan* plan, double* c_ms,
                      double* measured_ms, double* kernel_ms, int32_t* hit);
-/* Commit a plan with its measurement (measured_ms = 0 for a solve-only row); all-or-nothing. */
+/* Commit a plan with its measurement (measured_ms = 0 for a solve-only row); all-or-nothing.
+ * replayed = 1 marks a measurement parsed from a recorded program output rather than a device
+ * run (the CLI's --outcomes): the row is kept, and calibration leaves it out. */
 int uk_ledger_commit(void* ledger, const char* hcs_json, const char* kml_json, const uk_plan* plan,
-                     double measured_ms, double kernel_ms);
+                     double measured_ms, double kernel_ms, int32_t replayed);
 int uk_ledger_record_violation(void* ledger, const char* hcs_json, const char* kml_json, double rate,
                                double threshold, int32_t migrations, int32_t checks, uint64_t vram_free);
 int uk_ledger_size(void* ledger, int32_t* solutions, int32_t* violations);
@@ -283,6 +294,7 @@ int uk_memcpy_dtoh(void* dst, const void* src, size_t bytes);
 int uk_memset(void* p, int value, size_t bytes);
 int uk_synchronize(void);
 int uk_stream_create(void** stream);
+/* Synchronises the stream, frees the 1-D reduce partials uk_launch kept for it, destroys it. */
 int uk_stream_destroy(void* stream);
 int uk_stream_synchronize(void* stream);
 int uk_event_create(void** ev);

@@ -77,17 +77,25 @@ def test_f16_tn_exact_mode_bit_exact(gpu, vi):
     assert np.array_equal(C, O.f16_bits(R))
 
 
-def test_f16_tn_4096_cubed_rows(gpu):
-    # The config-3 shape through the solver's plan; checked on a row sample against the oracle.
+def test_f16_tn_4096_cubed_full(gpu):
+    # The config-3 shape through the solver's plan, every one of its 16.8 M outputs against the
+    # oracle (f32 accumulation over the same half inputs, k ascending; about 2 s on 16 host
+    # threads): the Frobenius gate over the whole matrix, and each 256 x 256 tile on its own, so a
+    # single wrong tile cannot hide in the whole-matrix norm.
     M = N = K = 4096
     A, B = f16_inputs(M, N, K, 20261201 + 20)
     sol = gpu.solve(gpu.make_desc("gemm", [M, N, K], dtype="fp16", layout="TN"))
     assert sol.family == "gemm_f16_mfma"
-    C = gemm_gpu(gpu, A, B, "fp16", "TN")
-    rows = np.array([0, 1, 255, 256, 1000, 2047, 2048, 3333, 4094, 4095])
-    R = O.gemm_f16q(A[rows], B, True)
-    assert frob(O.f16_to_f32(C[rows]), R) <= 1e-2
-    assert frob(O.f16_to_f32(C[rows]), R) <= 1e-3
+    C = O.f16_to_f32(gemm_gpu(gpu, A, B, "fp16", "TN"))
+    R = O.gemm_f16q(A, B, True, threads=16)
+    assert frob(C, R) <= 1e-2
+    # Both sides accumulate in f32; the only extra error is the final rounding to half.
+    assert frob(C, R) <= 1e-3
+    t = 256
+    per_tile = np.sqrt(((C.astype(np.float64) - R) ** 2).reshape(M // t, t, N // t, t).sum(axis=(1, 3)) /
+                       (R.astype(np.float64) ** 2).reshape(M // t, t, N // t, t).sum(axis=(1, 3)))
+    print(f"frobenius {frob(C, R):.3e}, worst tile {per_tile.max():.3e}")
+    assert per_tile.max() <= 1e-3
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 1, 1), (33, 47, 129), (100, 70, 5), (64, 64, 16), (257, 129, 300)])

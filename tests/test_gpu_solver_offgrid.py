@@ -4,16 +4,16 @@ the measured times of the compiled candidates).
 
 For each shape, the solver's pick and the next-best candidates of its own ranking run through
 uk_run (same seeded inputs, self-verified, settled kernel-only median). The numbers are printed;
-the assertion is deliberately loose (the pick within 15% of the fastest candidate measured), so a
-slower or faster box cannot fail it, while a cost model that ranks a clearly slower kernel first
-does. profiles/solver_offgrid.md holds a full sweep of every candidate at these shapes.
+the timing assertion (the pick within 15% of the fastest candidate measured) is a performance
+bound, not correctness, so the module carries the perf marker and stays out of -m gpu.
+profiles/solver_offgrid.md holds a full sweep of every candidate at these shapes.
 """
 import ctypes as C
 import re
 
 import pytest
 
-pytestmark = pytest.mark.gpu
+pytestmark = pytest.mark.perf
 
 _CAND = re.compile(r"candidate (\S+) family=(\d+) variant=(\d+) predicted_us=([0-9.eE+-]+)")
 

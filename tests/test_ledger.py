@@ -223,6 +223,37 @@ def test_calibrate_from_probe(uk, ledger_path):
         assert cal["clock_mhz"] == pytest.approx(2400 * 0.8, rel=1e-9)
 
 
+def test_calibrate_leaves_out_streamed_and_replayed_rows(uk, ledger_path):
+    # A streamed (scenario-B) GEMM row is priced as a pass of host copies overlapping shard
+    # kernels while its kernel_ms covers the shard kernels only: its c_ms / kernel_ms measures copy
+    # against kernel (here 15x), not the clock. Beside a resident streaming row (2x) the fit
+    # takes only the resident one; a row replayed from a recorded output is left out as well.
+    h = json.loads((ROOT / "samples" / "hcs_mi355x.json").read_text())
+    h["tiers"][0]["bytes"] = 96 << 20
+    hcs = json.dumps(h)
+    streamed = uk.solve(uk.kml_import(GEMM), hcs)
+    assert streamed.plan.shard_rows > 0
+    with uk.Ledger(ledger_path) as L:
+        _commit_ratio(uk, L, ROWSUM, hcs, 2.0)
+        k_ms = streamed.predicted_us * 1e-3 / 15.0
+        L.commit(GEMM, streamed.plan, measured_ms=20 * k_ms, kernel_ms=k_ms, hcs_json=hcs)
+        sm = uk.solve(uk.kml_import(SOFTMAX))  # a plan from the full tier; the small one cannot hold it
+        L.commit(SOFTMAX, sm.plan, measured_ms=sm.predicted_us * 1e-3 / 7.0, kernel_ms=sm.predicted_us * 1e-3 / 7.0,
+                 hcs_json=hcs, replayed=True)
+        assert L.lookup(SOFTMAX, hcs).measured_ms > 0  # the replayed row is kept for lookups
+        out, detail = L.calibrate(hcs)
+        cal = json.loads(out)
+        assert cal["hbm_bw_gbps"] == pytest.approx(2.0 * h["hbm_bw_gbps"], rel=1e-9)
+        assert cal["clock_mhz"] == h["clock_mhz"]  # no resident MFMA-bound row: the clock is kept
+        assert cal["link_bw_gbps"] == h["link_bw_gbps"]  # the streamed pass is not one host copy
+        assert "streaming: 1 row(s)" in detail and "matrix:" not in detail
+        assert "left out: 1 replayed row(s)" in detail and "left out: 1 streamed row(s)" in detail
+        # A resident GEMM row beside them is fitted as usual.
+        _commit_ratio(uk, L, '{"op": "gemm", "dtype": "fp16", "dims": [1024, 1024, 1024], "layout": "TN"}', hcs, 1.25)
+        cal = json.loads(L.calibrate(hcs)[0])
+        assert cal["clock_mhz"] == pytest.approx(1.25 * h["clock_mhz"], rel=1e-9)
+
+
 def test_streamed_plan_round_trips(uk, ledger_path):
     # A scenario-B plan's shard height is part of the recorded plan (placement text), so a ledger
     # hit runs the same streamed pass; rows written without it read back as resident.

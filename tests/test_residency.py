@@ -95,6 +95,21 @@ def test_payload_refused_before_inputs_or_device(uk):
     assert "stream_refused" not in r.log  # B + two shard pairs fit; stops at the device check
 
 
+def test_vram_unknown_refused_before_inputs_or_device(uk):
+    # An HCS without a vram tier cannot decide residency (src/codegen_hip.cpp:209-215, the tier
+    # read at :309): the run is refused with exit class 4 before any input is generated or the
+    # device touched. The import accepts such a description only as unified memory (a "unified"
+    # tier and no "vram" one, src/hcs.cpp:83-89); a caller-supplied plan gets past the solver.
+    h = json.loads((SAMPLES / "hcs_mi355x.json").read_text())
+    h["unified_memory"] = True
+    h["tiers"] = [{"name": "unified", "bytes": 309237645312, "bw_gbps": 8000, "confidence": "official"}]
+    d = uk.make_desc("rmsnorm", [4096, 4096])
+    r = uk.run(d, plan=uk.solve(d).plan, hcs_json=json.dumps(h))
+    assert r.exit_code == uk.UK_HIP_FAILURE and r.built and not r.ran
+    assert "UNIKERN_ERROR what=vram_unknown" in r.log
+    assert (r.checks, r.migrations, r.cpu_ms) == (-1, -1, -1.0)  # nothing probed, no CPU pass
+
+
 def test_streamed_plan_refused_when_shards_do_not_fit(uk):
     g = uk.make_desc("gemm", [4096, 4096, 4096], dtype="fp16", layout="TN")
     p = uk.solve(g, _tiny_hcs(100_000_000)).plan
@@ -120,9 +135,25 @@ def test_parse_result_line(uk):
     # A library result line round-trips through its own formatter.
     again = uk.parse_result(r.line, 0)
     assert (again.verified, again.kernel_ms, again.checks, again.plan_key) == (True, 0.024, 20, r.plan_key)
-    # Absent residency tokens keep the -1 sentinels; a FAIL verdict is not verified.
+    assert (again.cpu_ms, again.cpu_cores, again.cpu_outputs) == (-1.0, -1, -1)
+    # Absent residency and CPU tokens keep the -1 sentinels; a FAIL verdict is not verified.
     r = uk.parse_result("UNIKERN_RESULT backend=amd verify=FAIL max_rel=0.5 measured_ms=1 kernel_ms=0.5", 1)
     assert not r.verified and (r.migrations, r.checks) == (-1, -1) and r.exit_code == 1
+    assert (r.cpu_ms, r.cpu_cores, r.cpu_outputs) == (-1.0, -1, -1)
+
+
+def test_result_line_carries_cpu_tokens(uk):
+    # The CPU reference pass beside the device time: cpu_ms= and cpu_cores= (plus how many
+    # outputs that pass computed) are formatted and parsed back.
+    line = ("UNIKERN_RESULT backend=amd verify=PASS max_rel=1e-07 measured_ms=3.0 kernel_ms=0.1 mode=resident "
+            "payload_mb=96.0 perf=4096x4096x4096 dtype=fp16 migrations=0 checks=3 vram_free=1 vram_total=2 "
+            "gate=frobenius err=2e-04 tol=1e-02 achieved=1356.000 unit=TFLOP/s peak=2516.6 frac=0.5389 "
+            "plan=gemm_f16:256x256x64 cpu_ms=812.500 cpu_cores=16 cpu_outputs=131072")
+    r = uk.parse_result(line, 0)
+    assert (r.cpu_ms, r.cpu_cores, r.cpu_outputs) == (812.5, 16, 131072)
+    again = uk.parse_result(r.line, 0)
+    assert (again.cpu_ms, again.cpu_cores, again.cpu_outputs) == (812.5, 16, 131072)
+    assert " cpu_ms=812.500 cpu_cores=16 cpu_outputs=131072" in r.line
 
 
 def test_parse_refusal_line(uk):
@@ -224,3 +255,19 @@ def test_cli_threshold_validated_at_parse(uk, tmp_path, bad):
     rc, _, err = _run(uk, tmp_path, f, "--migration-threshold", bad)
     assert rc == 2 and "--migration-threshold must be a number >= 0" in err
     assert not (tmp_path / "l.jsonl").exists()
+
+
+def test_stream_gemm_checks_operands_before_the_call(uk):
+    # uk_stream_gemm copies rows straight out of the host arrays, so a short or mistyped array is
+    # refused on the Python side before the library (or the device) is reached.
+    import numpy as np
+
+    d = uk.make_desc("gemm", [256, 128, 64], dtype="fp16", layout="TN")
+    A = np.zeros((256, 64), np.uint16)
+    B = np.zeros((128, 64), np.uint16)
+    for a, b in ((A[:255], B), (A, B[:, :63]), (A.astype(np.float32), B), (A, np.zeros((64, 128), np.uint16))):
+        with pytest.raises(uk.UnikernError) as e:
+            uk.stream_gemm(d, a, b)
+        assert e.value.code == uk.UK_BAD_INVOCATION and "stream_gemm:" in str(e.value)
+    with pytest.raises(uk.UnikernError):
+        uk.stream_gemm(uk.make_desc("softmax", [16, 16]), A, B)

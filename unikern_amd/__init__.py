@@ -193,6 +193,9 @@ class RunOutcome:
     sets: int
     log: str
     line: str
+    cpu_ms: float = -1.0      # the run's own CPU reference pass (binary64, over the outputs it checks)
+    cpu_cores: int = -1       # host threads that pass ran on
+    cpu_outputs: int = -1     # outputs it computed (all, or the sampled rows/images)
     raw: Result = field(repr=False, default=None)
 
 
@@ -212,7 +215,7 @@ def _outcome(r: Result, rc: int, log: str) -> RunOutcome:
     return RunOutcome(bool(r.built), bool(r.ran), bool(r.verified), rc, r.max_rel, r.err_metric, r.tol, r.kernel_ms,
                       r.measured_ms, r.achieved, r.peak, r.frac, "mfma" if r.bound == 1 else "hbm", r.migrations,
                       r.checks, r.vram_free, r.vram_total, r.plan.key.decode(), FAMILIES.get(r.plan.family, "?"),
-                      r.sets, log, line.value.decode(), r)
+                      r.sets, log, line.value.decode(), r.cpu_ms, r.cpu_cores, r.cpu_outputs, r)
 
 
 def parse_result(program_output: str, exit_code: int) -> RunOutcome:
@@ -329,12 +332,23 @@ def synchronize():
 def stream_gemm(d: OpDesc, A: np.ndarray, B: np.ndarray, plan: Plan | None = None,
                 hcs_json: str | None = None) -> tuple[np.ndarray, float]:
     """Scenario-B GEMM on host operands (uk_stream_gemm): (C, pass_ms). A [M][K], B as the layout
-    says, both f16 bits (uint16) or f32; C comes back in the same element type."""
+    says ([K][N] NT, [N][K] TN), both f16 bits (uint16) or f32 as the descriptor's dtype says; C
+    comes back in the same element type. The library copies rows straight out of the arrays, so
+    their shapes and element type are checked against the descriptor first."""
+    if d.op != OPS["gemm"] or d.ndims != 3:
+        raise UnikernError(UK_BAD_INVOCATION, "stream_gemm: the descriptor is not a gemm [M, N, K]")
+    M, N, K = (int(d.dims[i]) for i in range(3))
+    want = {DTYPES["fp16"]: np.uint16, DTYPES["fp32"]: np.float32}.get(int(d.dtype))
+    if want is None:
+        raise UnikernError(UK_BAD_INVOCATION, "stream_gemm: only fp16 and fp32 GEMMs stream")
+    b_shape = (N, K) if d.layout == LAYOUTS["TN"] else (K, N)
+    for name, arr, shape in (("A", A, (M, K)), ("B", B, b_shape)):
+        if arr.dtype != want or tuple(arr.shape) != shape:
+            raise UnikernError(UK_BAD_INVOCATION, f"stream_gemm: {name} is {arr.dtype}{tuple(arr.shape)}, the "
+                                                  f"descriptor needs {np.dtype(want)}{shape}")
     A = np.ascontiguousarray(A)
     B = np.ascontiguousarray(B)
-    M = int(d.dims[0]) if d.ndims else A.shape[0]
-    N = int(d.dims[1])
-    Cm = np.empty((M, N), dtype=A.dtype)
+    Cm = np.empty((M, N), dtype=want)
     ms = C.c_double()
     _check(lib.uk_stream_gemm(None if hcs_json is None else _text(hcs_json), C.byref(d),
                               None if plan is None else C.byref(plan), A.ctypes.data_as(C.c_void_p),
@@ -416,9 +430,9 @@ class Ledger:
         return LedgerHit(p, c.value, m.value, k.value) if hit.value else None
 
     def commit(self, kml_text: str, plan: Plan, measured_ms: float = 0.0, kernel_ms: float = 0.0,
-               hcs_json: str | None = None):
+               hcs_json: str | None = None, replayed: bool = False):
         _check(lib.uk_ledger_commit(self._h, None if hcs_json is None else _text(hcs_json), _text(kml_text),
-                                    C.byref(plan), measured_ms, kernel_ms))
+                                    C.byref(plan), measured_ms, kernel_ms, 1 if replayed else 0))
 
     def record_violation(self, kml_text: str, rate: float, threshold: float, migrations: int, checks: int,
                          vram_free: int, hcs_json: str | None = None):

@@ -39,7 +39,8 @@ class Result(C.Structure):
                 ("checks", C.c_int32), ("vram_free", C.c_uint64), ("vram_total", C.c_uint64),
                 ("algo_bytes", C.c_int64), ("algo_flops", C.c_int64), ("weight_bytes", C.c_int64),
                 ("launches", C.c_int32), ("repeats", C.c_int32), ("sets", C.c_int32), ("plan", Plan),
-                ("mode", C.c_char * 16), ("dtype", C.c_char * 8), ("perf", C.c_char * 48)]
+                ("mode", C.c_char * 16), ("dtype", C.c_char * 8), ("perf", C.c_char * 48),
+                ("cpu_ms", C.c_double), ("cpu_cores", C.c_int32), ("cpu_outputs", C.c_int64)]
 
 
 class MfmaProbe(C.Structure):
@@ -86,7 +87,7 @@ _SIG = {
     "uk_ledger_key": ([C.c_char_p, C.c_char_p, C.c_char_p, C.c_size_t], C.c_int),
     "uk_ledger_lookup": ([_P, C.c_char_p, C.c_char_p, C.POINTER(Plan), C.POINTER(C.c_double), C.POINTER(C.c_double),
                           C.POINTER(C.c_double), C.POINTER(C.c_int32)], C.c_int),
-    "uk_ledger_commit": ([_P, C.c_char_p, C.c_char_p, C.POINTER(Plan), C.c_double, C.c_double], C.c_int),
+    "uk_ledger_commit": ([_P, C.c_char_p, C.c_char_p, C.POINTER(Plan), C.c_double, C.c_double, C.c_int32], C.c_int),
     "uk_ledger_record_violation": ([_P, C.c_char_p, C.c_char_p, C.c_double, C.c_double, C.c_int32, C.c_int32,
                                     C.c_uint64], C.c_int),
     "uk_ledger_size": ([_P, C.POINTER(C.c_int32), C.POINTER(C.c_int32)], C.c_int),

@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cinttypes>
 #include <cmath>
 #include <cstdio>
@@ -191,18 +192,20 @@ size_t scratch_bytes(const KmlTree& t) {
 }
 
 // uk_launch's scratch: one buffer per (device, stream), allocated on the first launch on that
-// stream that needs one and kept for the process lifetime. Launches on one stream execute in
-// order, so they never overlap on one buffer; launches on different streams get different
-// buffers. (A stream destroyed while a launch on it is pending and a new stream created at the
-// same handle would share one; callers synchronise a stream before destroying it.)
+// stream that needs one. Launches on one stream execute in order, so they never overlap on one
+// buffer; launches on different streams get different buffers. uk_stream_destroy synchronises
+// its stream and frees that stream's buffer before destroying it, so a handle the runtime
+// recycles starts without one. A stream created outside the library keeps its buffer (8 KiB)
+// until the process ends.
+std::mutex g_scratch_mu;
+std::map<std::pair<int, hipStream_t>, Scratch> g_stream_scratch;
+
 int stream_scratch(hipStream_t stream, size_t need, Scratch* out) {
-  static std::mutex mu;
-  static std::map<std::pair<int, hipStream_t>, Scratch> bufs;
   if (need == 0) return UK_OK;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return fail(UK_HIP_FAILURE, "UNIKERN_ERROR what=hipGetDevice");
-  std::lock_guard<std::mutex> lk(mu);
-  Scratch& slot = bufs[{dev, stream}];
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  Scratch& slot = g_stream_scratch[{dev, stream}];
   if (slot.bytes < need) {
     void* q = nullptr;
     const hipError_t e = hipMalloc(&q, need);
@@ -583,7 +586,21 @@ struct RunData {
   int tol_kind = 0;
   double tol = 0;
   bool exact = false;
+  // the CPU reference pass: wall time, host threads, outputs computed
+  double cpu_ms = 0;
+  int cpu_threads = 1;
+  int64_t cpu_outputs = 0;
 };
+
+// Run one CPU reference computation over n independent units (rows, columns, planes) and record
+// its wall time and the host threads it ran on (ref_threads: what the reference loops use).
+template <typename F>
+void timed_ref(RunData* rd, int64_t units, F&& f) {
+  const auto t0 = std::chrono::steady_clock::now();
+  f();
+  rd->cpu_ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+  rd->cpu_threads = std::max(rd->cpu_threads, ref_threads(units));
+}
 
 double peak_of(const Hcs& h, const KmlTree& t, int* bound) {
   const bool mfma = t.op == OpKind::Gemm && t.dtype != DType::Q8_0;
@@ -636,13 +653,13 @@ void make_inputs(const KmlTree& t, uint64_t seed, bool exact, RunData* rd) {
         rd->out_bytes = size_t(s.L) * 4;
         rd->ref.resize(size_t(s.L));
         rd->row_abs.resize(size_t(s.L));
-        ref_rowsum(X, rd->ref.data(), rd->row_abs.data(), s.L, s.C);
+        timed_ref(rd, s.L, [&] { ref_rowsum(X, rd->ref.data(), rd->row_abs.data(), s.L, s.C); });
         rd->tol_kind = 1;
         rd->tol = 1e-5;
       } else if (t.op == OpKind::Softmax) {
         rd->out_bytes = size_t(n) * 4;
         rd->ref.resize(size_t(n));
-        ref_softmax(X, rd->ref.data(), s.L, s.C);
+        timed_ref(rd, s.L, [&] { ref_softmax(X, rd->ref.data(), s.L, s.C); });
         rd->tol_kind = 0;
         rd->tol = 1e-5;
       } else {
@@ -658,12 +675,14 @@ void make_inputs(const KmlTree& t, uint64_t seed, bool exact, RunData* rd) {
         rd->out_bytes = size_t(n) * 4;
         rd->ref.resize(size_t(n));
         if (t.op == OpKind::RmsNorm) {
-          ref_rmsnorm(rd->ins[0].as<float>(), W, rd->ref.data(), s.L, s.C, double(t.eps));
+          timed_ref(rd, s.L, [&] { ref_rmsnorm(rd->ins[0].as<float>(), W, rd->ref.data(), s.L, s.C, double(t.eps)); });
           rd->tol_kind = 0;
           rd->tol = 1e-5;
         } else {
           const float* Xc = rd->ins[0].as<float>();
-          for (int64_t i = 0; i < n; ++i) rd->ref[size_t(i)] = double(Xc[i] * W[i % s.C]);
+          timed_ref(rd, 1, [&] {
+            for (int64_t i = 0; i < n; ++i) rd->ref[size_t(i)] = double(Xc[i] * W[i % s.C]);
+          });
           rd->tol_kind = 3;
           rd->tol = 0;
         }
@@ -693,7 +712,8 @@ void make_inputs(const KmlTree& t, uint64_t seed, bool exact, RunData* rd) {
         rd->ins.push_back(std::move(w));
         rd->out_bytes = size_t(s.M * s.N) * 4;
         rd->ref.resize(size_t(s.M * s.N));
-        ref_q8_0(rd->ins[0].as<uint16_t>(), rd->ins[1].as<uint8_t>(), rd->ref.data(), s.M, s.N, s.K);
+        timed_ref(rd, s.N,
+                  [&] { ref_q8_0(rd->ins[0].as<uint16_t>(), rd->ins[1].as<uint8_t>(), rd->ref.data(), s.M, s.N, s.K); });
         rd->tol_kind = 2;
         rd->tol = 1e-5;
         break;
@@ -739,7 +759,7 @@ void make_inputs(const KmlTree& t, uint64_t seed, bool exact, RunData* rd) {
       rd->out_bytes = size_t(s.M * s.N) * (f16 ? 2 : 4);
       const std::vector<int64_t> rows = sample_rows(s.M, exact ? 64 : 32);
       rd->ref.resize(rows.size() * size_t(s.N));
-      ref_gemm(A.data(), B.data(), rd->ref.data(), s.M, s.N, s.K, bt, rows);
+      timed_ref(rd, int64_t(rows.size()), [&] { ref_gemm(A.data(), B.data(), rd->ref.data(), s.M, s.N, s.K, bt, rows); });
       for (int64_t r : rows)
         for (int64_t n = 0; n < s.N; ++n) rd->ref_index.push_back(size_t(r * s.N + n));
       if (exact) {
@@ -782,14 +802,18 @@ void make_inputs(const KmlTree& t, uint64_t seed, bool exact, RunData* rd) {
         std::vector<int64_t> ims = {0};
         if (s.Nb > 1) ims.push_back(s.Nb - 1);
         rd->ref.resize(ims.size() * size_t(s.Co * plane));
-        ref_conv_nchw(rd->ins[0].as<float>(), rd->ins[1].as<float>(), sc, rd->ref.data(), s.Nb, s.Ci, s.H, s.W, s.Co,
-                      s.Kh, s.Kw, s.pad, s.stride, ims);
+        timed_ref(rd, int64_t(ims.size()) * s.Co, [&] {
+          ref_conv_nchw(rd->ins[0].as<float>(), rd->ins[1].as<float>(), sc, rd->ref.data(), s.Nb, s.Ci, s.H, s.W, s.Co,
+                        s.Kh, s.Kw, s.pad, s.stride, ims);
+        });
         for (int64_t n : ims)
           for (int64_t i = 0; i < s.Co * plane; ++i) rd->ref_index.push_back(size_t(n * s.Co * plane + i));
       } else {
         rd->ref.resize(size_t(s.Co * plane));
-        ref_conv_hwc(rd->ins[0].as<float>(), rd->ins[1].as<float>(), sc, rd->ref.data(), s.H, s.W, s.Ci, s.Kh, s.Kw,
-                     s.Co);
+        timed_ref(rd, s.Co, [&] {
+          ref_conv_hwc(rd->ins[0].as<float>(), rd->ins[1].as<float>(), sc, rd->ref.data(), s.H, s.W, s.Ci, s.Kh, s.Kw,
+                       s.Co);
+        });
       }
       rd->tol_kind = exact ? 3 : 2;
       rd->tol = exact ? 0 : 1e-5;
@@ -1133,11 +1157,12 @@ int uk_format_result(const uk_result* r, char* line, size_t cap) {
   std::snprintf(b, sizeof b,
                 "UNIKERN_RESULT backend=amd verify=%s max_rel=%.6e measured_ms=%.6f kernel_ms=%.6f mode=%s "
                 "payload_mb=%.6f perf=%s dtype=%s migrations=%d checks=%d vram_free=%" PRIu64 " vram_total=%" PRIu64
-                " gate=%s err=%.6e tol=%.6e achieved=%.3f unit=%s peak=%.1f frac=%.4f plan=%s",
+                " gate=%s err=%.6e tol=%.6e achieved=%.3f unit=%s peak=%.1f frac=%.4f plan=%s cpu_ms=%.3f cpu_cores=%d"
+                " cpu_outputs=%" PRId64,
                 r->verified ? "PASS" : "FAIL", r->max_rel, r->measured_ms, r->kernel_ms, r->mode,
                 double(r->algo_bytes) / (1024.0 * 1024.0), r->perf, r->dtype, r->migrations, r->checks, r->vram_free,
                 r->vram_total, tk[std::min(std::max(r->tol_kind, 0), 3)], r->err_metric, r->tol, r->achieved, unit,
-                r->peak, r->frac, r->plan.key);
+                r->peak, r->frac, r->plan.key, r->cpu_ms, r->cpu_cores, r->cpu_outputs);
   return put(b, line, cap);
 }
 
@@ -1200,6 +1225,11 @@ int uk_parse_result(const char* program_output, int32_t exit_code, uk_result* ou
   std::snprintf(out->dtype, sizeof out->dtype, "%s", token(line, "dtype").c_str());
   std::snprintf(out->perf, sizeof out->perf, "%s", token(line, "perf").c_str());
   std::snprintf(out->plan.key, sizeof out->plan.key, "%s", token(line, "plan").c_str());
+  // The CPU tokens are this build's additions to the reference's line: optional (-1 if absent).
+  const std::string cms = token(line, "cpu_ms"), ccores = token(line, "cpu_cores"), couts = token(line, "cpu_outputs");
+  out->cpu_ms = cms.empty() ? -1.0 : std::atof(cms.c_str());
+  out->cpu_cores = ccores.empty() ? -1 : std::atoi(ccores.c_str());
+  out->cpu_outputs = couts.empty() ? -1 : std::strtoll(couts.c_str(), nullptr, 10);
   take_residency(line);
   return UK_OK;
 }
@@ -1227,6 +1257,9 @@ int uk_run(const char* hcs_json, const uk_op_desc* d, const uk_plan* plan, uint6
   std::memset(out, 0, sizeof *out);
   out->migrations = -1;
   out->checks = -1;
+  out->cpu_ms = -1;  // no CPU pass yet (a refusal ends before it)
+  out->cpu_cores = -1;
+  out->cpu_outputs = -1;
   std::ostringstream lg;
   auto finish = [&](int code) {
     out->exit_code = code;
@@ -1252,7 +1285,9 @@ int uk_run(const char* hcs_json, const uk_op_desc* d, const uk_plan* plan, uint6
   // payload beyond 0.85 of the device tier is refused rather than paged. The solver's capacity
   // predicate does not see a caller-supplied plan, so this check is the one that always runs. A
   // streamed GEMM plan (scenario B) keeps only B and two shard pairs on the device.
-  const double vram = double(h.device_capacity());
+  // The device tier is the HCS's "vram" tier, as the reference's emitter reads it
+  // (src/codegen_hip.cpp:309, :801, :1038): a unified-memory description has none.
+  const double vram = double(h.tier_bytes("vram"));
   if (vram <= 0) {
     g_err = "UNIKERN_ERROR what=vram_unknown (no device tier in the HCS: residency cannot be decided)";
     return finish(UK_HIP_FAILURE);
@@ -1294,6 +1329,11 @@ int uk_run(const char* hcs_json, const uk_op_desc* d, const uk_plan* plan, uint6
 
   RunData rd;
   make_inputs(t, seed, input_mode == UK_INPUTS_EXACT, &rd);
+  out->cpu_ms = rd.cpu_ms;
+  out->cpu_cores = rd.cpu_threads;
+  out->cpu_outputs = int64_t(rd.ref.size());
+  lg << "UNIKERN_INFO cpu_reference binary64 outputs=" << rd.ref.size() << " of " << rd.out_bytes / (rd.out_kind ? 2 : 4)
+     << " threads=" << rd.cpu_threads << " ms=" << rd.cpu_ms << "\n";
   if (streamed) {
     // Scenario B (reference src/codegen_hip.cpp:1480-1708): verify one streamed pass, time
     // passes end to end (measured_ms) and the shards' kernels on resident buffers (kernel_ms).
@@ -1602,7 +1642,23 @@ int uk_synchronize(void) { return hip_rc(hipDeviceSynchronize(), "hipDeviceSynch
 int uk_stream_create(void** s) {
   return hip_rc(hipStreamCreate(reinterpret_cast<hipStream_t*>(s)), "hipStreamCreate");
 }
-int uk_stream_destroy(void* s) { return hip_rc(hipStreamDestroy(static_cast<hipStream_t>(s)), "hipStreamDestroy"); }
+int uk_stream_destroy(void* s) {
+  const hipStream_t st = static_cast<hipStream_t>(s);
+  if (st) {
+    // Pending launches may still use the stream's scratch: let them finish, then free it.
+    if (int rc = hip_rc(hipStreamSynchronize(st), "hipStreamSynchronize")) return rc;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    for (auto it = g_stream_scratch.begin(); it != g_stream_scratch.end();) {
+      if (it->first.second == st) {
+        if (it->second.ptr) (void)hipFree(it->second.ptr);
+        it = g_stream_scratch.erase(it);
+      } else {
+        ++it;
+      }
+    }
+  }
+  return hip_rc(hipStreamDestroy(st), "hipStreamDestroy");
+}
 int uk_stream_synchronize(void* s) {
   return hip_rc(hipStreamSynchronize(static_cast<hipStream_t>(s)), "hipStreamSynchronize");
 }
@@ -1685,7 +1741,7 @@ int uk_ledger_lookup(void* ledger, const char* hcs_json, const char* kml_json, u
 }
 
 int uk_ledger_commit(void* ledger, const char* hcs_json, const char* kml_json, const uk_plan* plan,
-                     double measured_ms, double kernel_ms) {
+                     double measured_ms, double kernel_ms, int32_t replayed) {
   if (!ledger || !plan) return fail(UK_BAD_INVOCATION, "null argument");
   LedgerKey k;
   if (!ledger_key_of(hcs_json, kml_json, &k, nullptr)) return UK_BAD_INVOCATION;
@@ -1697,7 +1753,8 @@ int uk_ledger_commit(void* ledger, const char* hcs_json, const char* kml_json, c
   r.tile_n = plan->tile_n;
   r.placement = placement_of(std::string(plan->key, strnlen(plan->key, sizeof plan->key)), plan->family,
                              plan->variant, plan->shard_rows,
-                             "grid=" + std::to_string(plan->grid) + " threads=" + std::to_string(plan->threads));
+                             std::string(replayed ? kReplayedTag : "") + "grid=" + std::to_string(plan->grid) +
+                                 " threads=" + std::to_string(plan->threads));
   std::string e;
   if (!as_ledger(ledger)->commit(k, r, &e)) return fail(UK_HIP_FAILURE, e);
   return UK_OK;

@@ -275,7 +275,7 @@ int cmd_solve(int argc, char** argv) {
             << s.log << "\n";
   print_coverage(gap);
   // solve has no measurement: the row carries the prediction, replaced by run's measurement.
-  if (uk_ledger_commit(ledger, hcs_arg(hcs), kml.c_str(), &s.plan, s.plan.predicted_us * 1e-3, 0.0) != UK_OK)
+  if (uk_ledger_commit(ledger, hcs_arg(hcs), kml.c_str(), &s.plan, s.plan.predicted_us * 1e-3, 0.0, 0) != UK_OK)
     std::cerr << "ledger commit failed: " << last_error() << "\n";
   uk_ledger_close(ledger);
   if (o.selfcheck) {  // solve is a pure function of (hcs, tree)
@@ -470,7 +470,9 @@ int cmd_run(int argc, char** argv, bool write_ledger) {
     uk_ledger_close(ledger);
     return 0;
   }
-  if (uk_ledger_commit(ledger, hcs_arg(used_hcs), kml.c_str(), &plan, x.r.measured_ms, x.r.kernel_ms) != UK_OK) {
+  // A measurement parsed from a recorded output (--outcomes) is committed as replayed.
+  if (uk_ledger_commit(ledger, hcs_arg(used_hcs), kml.c_str(), &plan, x.r.measured_ms, x.r.kernel_ms, rp ? 1 : 0) !=
+      UK_OK) {
     std::cerr << "ledger commit failed: " << last_error() << "\n";
     uk_ledger_close(ledger);
     return 2;

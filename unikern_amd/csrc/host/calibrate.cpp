@@ -11,6 +11,8 @@
 //  * With no MFMA-bound row, a matrix-core probe supplies the clock factor instead: the variant
 //    efficiencies were fitted on parts whose probe sustained kEffFitProbeClockGhz, so a part that
 //    sustains less under the same load runs every MFMA-bound plan proportionally slower.
+//  * Streamed (scenario-B) rows and rows replayed from recorded outputs take no part in the fit:
+//    the first are priced as copies overlapping shard kernels, the second were not measured here.
 //  * The end-to-end time of a row minus its kernel time is the host copy of its inputs and
 //    outputs. A straight line copy_ms = latency + bytes / link through all usable rows (ordinary
 //    least squares; a single byte count gives the zero-latency ratio) separates the per-call
@@ -50,9 +52,22 @@ Calibration calibrate_hcs(const Hcs& in, const std::vector<LedgerMeasured>& rows
   Calibration c;
   c.hcs = in;
   std::vector<double> stream_ratio, mfma_ratio, link_x, link_y;
+  int streamed = 0, replayed = 0;
   for (const LedgerMeasured& r : rows) {
     const auto t = tree_from_signature(r.op_sig);
     if (!t) continue;
+    // A replayed row was parsed from a recorded output, not measured here. A streamed row's
+    // prediction is a pass of overlapping host copies and shard kernels, while its kernel_ms covers
+    // the shard kernels only, so its ratio measures copy against kernel, not the clock or the
+    // HBM rate, and its end-to-end time is not one copy of its inputs and outputs.
+    if (r.replayed) {
+      ++replayed;
+      continue;
+    }
+    if (r.shard_rows > 0) {
+      ++streamed;
+      continue;
+    }
     if (r.c_ms > 0 && r.kernel_ms > 0 && std::isfinite(r.c_ms / r.kernel_ms))
       (mfma_bound(*t) ? mfma_ratio : stream_ratio).push_back(r.c_ms / r.kernel_ms);
     const double copy_ms = r.measured_ms - r.kernel_ms;
@@ -63,6 +78,10 @@ Calibration calibrate_hcs(const Hcs& in, const std::vector<LedgerMeasured>& rows
     }
   }
   std::ostringstream d;
+  if (replayed) d << "left out: " << replayed << " replayed row(s) (recorded outputs, not device measurements)\n";
+  if (streamed)
+    d << "left out: " << streamed << " streamed row(s) (pass of host copies and shard kernels; not a clock, HBM or "
+         "link figure)\n";
 
   if (!stream_ratio.empty() && in.hbm_bw_gbps > 0) {
     c.hbm_rows = int(stream_ratio.size());

@@ -94,11 +94,15 @@ void q8_0_pack(const int8_t* q, const uint16_t* d, uint8_t* blocks, int N, int K
     }
 }
 
+int ref_threads(int64_t n) {
+  if (n < 64) return 1;
+  return int(std::min<unsigned>(std::max(1u, std::thread::hardware_concurrency()), 32u));
+}
+
 namespace {
 template <typename F>
 void parallel_for(int64_t n, F&& f) {
-  int th = int(std::min<unsigned>(std::max(1u, std::thread::hardware_concurrency()), 32u));
-  if (n < 64) th = 1;
+  const int th = ref_threads(n);
   std::vector<std::thread> ts;
   for (int t = 1; t < th; ++t) ts.emplace_back([&, t] { f(n * t / th, n * (t + 1) / th); });
   f(0, n / th);

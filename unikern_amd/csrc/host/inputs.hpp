@@ -36,6 +36,9 @@ enum SeedOffset : uint64_t {
 };
 
 // ---- binary64 references for the self-check ----
+// Host threads the reference loops below run on for n independent units (rows, columns,
+// planes): min(hardware threads, 32), or 1 below 64 units.
+int ref_threads(int64_t n);
 void ref_rowsum(const float* X, double* Y, double* Yabs, int64_t L, int64_t C);
 void ref_rmsnorm(const float* X, const float* W, double* Y, int64_t L, int64_t C, double eps);
 void ref_softmax(const float* X, double* Y, int64_t L, int64_t C);

@@ -4,8 +4,10 @@
 #include <dlfcn.h>
 
 #include <cstdio>
+#include <cstring>
 #include <fstream>
 #include <limits>
+#include <map>
 #include <sstream>
 
 namespace uk {
@@ -99,7 +101,9 @@ class FileLedger : public Ledger {
   }
 
   std::vector<LedgerMeasured> measured_rows(const std::string& hcs_fp) override {
-    std::vector<LedgerMeasured> out;
+    // The latest line of each key, as lookup reads it (a replacement appends a new line).
+    std::vector<std::string> order;
+    std::map<std::string, LedgerMeasured> latest;
     std::ifstream in(path_);
     std::string line;
     while (std::getline(in, line)) {
@@ -112,8 +116,13 @@ class FileLedger : public Ledger {
       m.op_sig = f[0].substr(0, p1);
       if (!to_double(f[1], &m.c_ms) || !to_double(f[2], &m.measured_ms)) continue;
       if (f.size() >= 7 && !to_double(f[3], &m.kernel_ms)) continue;
-      if (m.measured_ms > 0) out.push_back(m);
+      placement_flags(f.size() >= 7 ? f[6] : f.size() >= 6 ? f[5] : f[3], &m.shard_rows, &m.replayed);
+      if (!latest.count(f[0])) order.push_back(f[0]);
+      latest[f[0]] = m;
     }
+    std::vector<LedgerMeasured> out;
+    for (const std::string& k : order)
+      if (latest[k].measured_ms > 0) out.push_back(latest[k]);
     return out;
   }
 
@@ -353,8 +362,8 @@ class SqliteLedger : public Ledger {
     std::vector<LedgerMeasured> out;
     void* st = nullptr;
     if (a.prepare(db_,
-                  "SELECT op_sig, c_ms, measured_ms, kernel_ms FROM solutions WHERE hcs_fp = ?1 AND measured_ms > 0 "
-                  "ORDER BY key",
+                  "SELECT op_sig, c_ms, measured_ms, kernel_ms, placement FROM solutions WHERE hcs_fp = ?1 AND "
+                  "measured_ms > 0 ORDER BY key",
                   -1, &st, nullptr) != SqliteApi::kOk)
       return out;
     a.bind_text(st, 1, hcs_fp.c_str(), -1, kTransient);
@@ -365,6 +374,8 @@ class SqliteLedger : public Ledger {
       m.c_ms = a.col_double(st, 1);
       m.measured_ms = a.col_double(st, 2);
       m.kernel_ms = a.col_double(st, 3);
+      const unsigned char* pl = a.col_text(st, 4);
+      placement_flags(pl ? reinterpret_cast<const char*>(pl) : "", &m.shard_rows, &m.replayed);
       out.push_back(m);
     }
     a.finalize(st);
@@ -424,6 +435,14 @@ std::string placement_of(const std::string& plan_key, int family, int variant, i
   std::string p = "plan=" + plan_key + " family=" + std::to_string(family) + " variant=" + std::to_string(variant);
   if (shard_rows > 0) p += " shard_rows=" + std::to_string(shard_rows);
   return p + " | " + why;
+}
+
+void placement_flags(const std::string& placement, int* shard_rows, bool* replayed) {
+  std::string key;
+  int family = 0, variant = 0;
+  if (!parse_placement(placement, &key, &family, &variant, shard_rows)) *shard_rows = 0;
+  const size_t bar = placement.find(" | ");
+  *replayed = bar != std::string::npos && placement.compare(bar + 3, std::strlen(kReplayedTag), kReplayedTag) == 0;
 }
 
 bool parse_placement(const std::string& placement, std::string* plan_key, int* family, int* variant,

@@ -34,7 +34,12 @@ struct LedgerRow {
 struct LedgerMeasured {
   std::string op_sig;
   double c_ms = 0, measured_ms = 0, kernel_ms = 0;
+  int shard_rows = 0;     // > 0: a streamed (scenario-B) plan, priced as copies overlapping shard kernels
+  bool replayed = false;  // parsed from a recorded program output, not measured on a device
 };
+
+// Marks the "why" part of a placement whose measurement was replayed from a recorded output.
+inline constexpr const char* kReplayedTag = "replayed ";
 
 class Ledger {
  public:
@@ -58,5 +63,7 @@ std::string placement_of(const std::string& plan_key, int family, int variant, i
                          const std::string& why);
 bool parse_placement(const std::string& placement, std::string* plan_key, int* family, int* variant,
                      int* shard_rows);
+// shard_rows and the replayed mark of a placement text (0 / false when it has neither).
+void placement_flags(const std::string& placement, int* shard_rows, bool* replayed);
 
 }  // namespace uk
