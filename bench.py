@@ -509,6 +509,9 @@ def main():
     ap.add_argument("--sets", type=int, default=7, help=argparse.SUPPRESS)
     ap.add_argument("--vendor-gemm", action="store_true",
                     help="also time the f16 GEMM through torch.mm (hipBLASLt) on the same inputs, for context")
+    ap.add_argument("--only", choices=["gemm", "gemm_f32", "copy", "conv", "q8_0"], default=None,
+                    help="time one secondary family alone and print its results (for counter passes); not the "
+                         "bench line")
     ap.add_argument("--settle-ms", type=float, default=50.0,
                     help="untimed run of each kernel before its warm-up steps (0: none; counter passes use 0)")
     args = ap.parse_args()
@@ -529,6 +532,13 @@ def main():
     uk.device_check()
     stream = C.c_void_p()
     uk._check(uk.lib.uk_stream_create(C.byref(stream)))
+    if args.only:
+        sec_steps, sec_warm = max(10, args.steps // 2), max(5, args.warmup // 2)
+        fn = {"gemm": bench_gemm, "gemm_f32": bench_gemm_f32, "copy": bench_copy, "conv": bench_conv}.get(args.only)
+        res = fn(uk, O, sec_steps, sec_warm, stream) if fn else bench_q8(uk, O, args.steps, args.warmup, stream)
+        uk.lib.uk_stream_destroy(stream)
+        print(json.dumps({"only": args.only, "results": res if isinstance(res, list) else [res]}), flush=True)
+        return
 
     stats, total_ms, wall_ms, step_bytes, verified, sets = bench_rows(uk, O, args.steps, args.warmup, stream)
     value = step_bytes / (total_ms * 1e-3) / 1e9

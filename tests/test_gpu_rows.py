@@ -152,6 +152,20 @@ def test_softmax_large_magnitudes_need_max_subtraction(gpu):
     check_rows_op(Y, O.softmax(X), softmax64(X), C)
 
 
+@pytest.mark.parametrize("vi", [11, 17, 24])
+def test_softmax_huge_maxima_take_the_exact_path(gpu, vi):
+    # The numerators are 2^(x log2 e - max log2 e) with max log2 e rounded once per row; a row
+    # whose maximum is 1.16e7 or more (max log2 e >= 2^24) takes e^(x - max) on the exact path
+    # instead. Rows on either side of that edge, and far beyond it, share one launch.
+    L, C = 12, 4096
+    X = O.normal(L * C, 77, 0.0, 8.0).reshape(L, C)
+    offsets = np.array([0, 1e4, -1e6, 1.1e7, 1.17e7, -1.17e7, 1e8, -3e9, 1e20, -1e30, 250.0, 0], np.float32)
+    X = (X + offsets[:, None]).astype(np.float32)
+    Y = run_op(gpu, "softmax", X, plan=rows_plan(gpu, vi))
+    assert np.all(np.isfinite(Y))
+    check_rows_op(Y, O.softmax(X), softmax64(X), C)
+
+
 @pytest.mark.parametrize("L,C", [(4096, 4096), (65536, 256), (3, 7), (1, 1), (5, 12), (37, 4096), (6, 2052),
                                  (5, 3000), (2, 2048), (3, 4100)])
 def test_channelscale_bit_exact(gpu, L, C):

@@ -11,9 +11,10 @@
 //
 // Semantics kept from the reference CPU loops: rmsnorm y = (x * rms) * W with
 // rms = 1/sqrt(sum(x^2)/C + eps) (correctly rounded divide and sqrt); softmax
-// y = exp(x - max) / sum(exp(x - max)), here as exp(x - max) * (1 / sum) with a 1.23-ulp exp:
-// within a few roundings of the reference, far inside the 1e-5 relative gate, and half the
-// vector instructions of a libm exp and a divide per element (those did not hide behind HBM).
+// y = exp(x - max) / sum(exp(x - max)), here as 2^(x log2 e - max log2 e) * (1 / sum) on
+// v_exp_f32 (exp_row below): within about 2e-6 of the reference wherever the 1e-5 relative gate
+// can see an element, and a fifth of the vector instructions of a libm exp and a divide per
+// element (those did not hide behind HBM).
 #include <math.h>
 
 #include "../launch.hpp"
@@ -34,17 +35,29 @@ __device__ __forceinline__ void st4(f32x4* p, f32x4 v) {
   else *p = v;
 }
 
-// e^d for the softmax numerators: 2^(d log2 e) on v_exp_f32, with the rounding error of the
-// product d * log2(e) (recovered exactly by an fma) and the tail of log2(e) folded back in as
-// 2^p * (1 + err * ln 2). Measured against binary64 on the device: at most 1.23 ulp over the
-// normal range d in [-87.3, 0]; e^-inf = 0; NaN propagates. libm's expf costs about three
-// times the instructions, which the softmax kernel cannot hide behind its HBM stream.
+// e^(x - m) for the softmax numerators of a row with maximum m, given mL = m * log2(e) rounded
+// once per row: 2^t with t = x * log2(e) - mL from one fma (exact product, one rounding) on
+// v_exp_f32. The rounding of mL scales every numerator of the row, and so the row sum, by the
+// same factor, which cancels in the quotient. What remains per element is the fma's rounding and
+// the binary32 log2(e), each at most |t| * 2^-24 in t, plus v_exp_f32's own error. Only elements
+// with e^(x - m) >= 1e-6 * sum (so t >= -20) can move the 1e-5 relative gate (whose denominator
+// is max(|r|, 1e-6)): for them the numerator is within 2 * 20 * 2^-24 * ln 2 + 2^-23, about 1.8e-6
+// relative, of e^(x - m). The row factor is 2^e with |e| at most one ulp of mL: rows with
+// |mL| < 2^24 (|m| < 1.16e7) keep it within [1/2, 2], so nothing overflows or underflows that the
+// reference keeps; larger or non-finite maxima take exp_softmax(x - m) instead. Padding (-inf)
+// gives 0.
+constexpr float kLog2eF = 1.44269502f;  // log2(e) rounded to binary32
+__device__ __forceinline__ float exp_row(float x, float mL) { return __builtin_amdgcn_exp2f(fmaf(x, kLog2eF, -mL)); }
+
+// e^d on v_exp_f32 with the rounding error of the product d * log2(e) (recovered exactly by an
+// fma) and the tail of log2(e) folded back in as 2^p * (1 + err * ln 2): at most 1.23 ulp against
+// binary64 over d in [-87.3, 0] (measured on the device); e^-inf = 0; NaN propagates. The softmax
+// of a row whose maximum is beyond exp_row's range.
 __device__ __forceinline__ float exp_softmax(float d) {
-  constexpr float kLog2e = 1.44269502f;          // log2(e) rounded to binary32
-  constexpr float kLog2eTail = 1.925963033e-8f;  // log2(e) - kLog2e
+  constexpr float kLog2eTail = 1.925963033e-8f;  // log2(e) - kLog2eF
   constexpr float kLn2 = 0.693147181f;
-  const float p = d * kLog2e;
-  const float err = fmaf(d, kLog2eTail, fmaf(d, kLog2e, -p));
+  const float p = d * kLog2eF;
+  const float err = fmaf(d, kLog2eTail, fmaf(d, kLog2eF, -p));
   const float r = __builtin_amdgcn_exp2f(p);
   return (r == 0.f) ? 0.f : fmaf(r, err * kLn2, r);
 }
@@ -203,14 +216,27 @@ __global__ void __launch_bounds__(TPR < 256 ? 256 : TPR)
 #pragma unroll
       for (int i = 0; i < NV; ++i) m = fmaxf(m, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
       m = row_reduce_max(m, red0[k & 1]);
+      // A wavefront holds part of one row only (TPR >= 64), so m is uniform: branch on a scalar.
+      const float mL = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, m * kLog2eF)));
       float s = 0.f;
+      if (__builtin_fabsf(mL) < 0x1p24f) {
 #pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        v[i].x = exp_softmax(v[i].x - m);
-        v[i].y = exp_softmax(v[i].y - m);
-        v[i].z = exp_softmax(v[i].z - m);
-        v[i].w = exp_softmax(v[i].w - m);
-        s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+        for (int i = 0; i < NV; ++i) {
+          v[i].x = exp_row(v[i].x, mL);
+          v[i].y = exp_row(v[i].y, mL);
+          v[i].z = exp_row(v[i].z, mL);
+          v[i].w = exp_row(v[i].w, mL);
+          s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          v[i].x = exp_softmax(v[i].x - m);
+          v[i].y = exp_softmax(v[i].y - m);
+          v[i].z = exp_softmax(v[i].z - m);
+          v[i].w = exp_softmax(v[i].w - m);
+          s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+        }
       }
       s = row_reduce_sum(s, red1[k & 1]);
       // One correctly rounded reciprocal per row, then a multiply per element: within one
