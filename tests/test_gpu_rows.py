@@ -153,10 +153,11 @@ def test_softmax_large_magnitudes_need_max_subtraction(gpu):
 
 
 @pytest.mark.parametrize("vi", [11, 17, 24])
-def test_softmax_huge_maxima_take_the_exact_path(gpu, vi):
-    # The numerators are 2^(x log2 e - max log2 e) with max log2 e rounded once per row; a row
-    # whose maximum is 1.16e7 or more (max log2 e >= 2^24) takes e^(x - max) on the exact path
-    # instead. Rows on either side of that edge, and far beyond it, share one launch.
+def test_softmax_huge_maxima(gpu, vi):
+    # The numerators are 2^((x - max) log2 e): x - max is exact wherever x is within a factor of
+    # two of the maximum, so their error does not grow with the maximum's magnitude. Rows with
+    # maxima from 0 to 1e30 (where max log2 e rounded to binary32 is off by up to 2^76) share one
+    # launch; variant 24 is the grouped-store form.
     L, C = 12, 4096
     X = O.normal(L * C, 77, 0.0, 8.0).reshape(L, C)
     offsets = np.array([0, 1e4, -1e6, 1.1e7, 1.17e7, -1.17e7, 1e8, -3e9, 1e20, -1e30, 250.0, 0], np.float32)

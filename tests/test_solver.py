@@ -168,10 +168,10 @@ def test_argmin_is_deterministic_under_candidate_ties(uk):
 
 def test_calibrated_rows_picks(uk):
     # The per-op efficiencies measured at 4096 x 4096 decide: the non-temporal 512-thread variant
-    # for row-sum and softmax, one wavefront per row with grouped stores for RMSNorm.
+    # for row-sum, one wavefront per row with grouped stores for RMSNorm and softmax.
     picks = {op: uk.solve(uk.make_desc(op, [4096, 4096])).key for op in ("reduce", "rmsnorm", "softmax")}
     assert picks == {"reduce": "rows:tpr=512,nv=2,nt", "rmsnorm": "rows:tpr=64,nv=16,nt,grp",
-                     "softmax": "rows:tpr=512,nv=2,nt"}
+                     "softmax": "rows:tpr=64,nv=16,nt,grp"}
 
 
 def _feasible_rows_keys(d):

@@ -11,11 +11,12 @@
 //
 // Semantics kept from the reference CPU loops: rmsnorm y = (x * rms) * W with
 // rms = 1/sqrt(sum(x^2)/C + eps) (correctly rounded divide and sqrt); softmax
-// y = exp(x - max) / sum(exp(x - max)), here as 2^(x log2 e - max log2 e) * (1 / sum) on
-// v_exp_f32 (exp_row below): within about 2e-6 of the reference wherever the 1e-5 relative gate
-// can see an element, and a fifth of the vector instructions of a libm exp and a divide per
-// element (those did not hide behind HBM).
+// y = exp(x - max) / sum(exp(x - max)), here as 2^((x - max) log2 e) * (1 / sum) on v_exp_f32
+// (exp_sub below): within about 2e-6 of the reference wherever the 1e-5 relative gate can see an
+// element, and a fifth of the vector instructions of a libm exp and a divide per element.
 #include <math.h>
+
+#include <mutex>
 
 #include "../launch.hpp"
 #include "../variants.hpp"
@@ -35,42 +36,31 @@ __device__ __forceinline__ void st4(f32x4* p, f32x4 v) {
   else *p = v;
 }
 
-// e^(x - m) for the softmax numerators of a row with maximum m, given mL = m * log2(e) rounded
-// once per row: 2^t with t = x * log2(e) - mL from one fma (exact product, one rounding) on
-// v_exp_f32. The rounding of mL scales every numerator of the row, and so the row sum, by the
-// same factor, which cancels in the quotient. What remains per element is the fma's rounding and
-// the binary32 log2(e), each at most |t| * 2^-24 in t, plus v_exp_f32's own error. Only elements
-// with e^(x - m) >= 1e-6 * sum (so t >= -20) can move the 1e-5 relative gate (whose denominator
-// is max(|r|, 1e-6)): for them the numerator is within 2 * 20 * 2^-24 * ln 2 + 2^-23, about 1.8e-6
-// relative, of e^(x - m). The row factor is 2^e with |e| at most one ulp of mL: rows with
-// |mL| < 2^24 (|m| < 1.16e7) keep it within [1/2, 2], so nothing overflows or underflows that the
-// reference keeps; larger or non-finite maxima take exp_softmax(x - m) instead. Padding (-inf)
-// gives 0.
+// e^(x - m) for the softmax numerators of a row with maximum m: 2^((x - m) log2 e) as a subtract,
+// a multiply by the binary32 log2(e) and v_exp_f32. Error in the exponent t = (x - m) log2 e: the
+// subtract's rounding (at most |x - m| 2^-24, none when x is within a factor of two of m), the
+// product's (|t| 2^-24) and the binary32 log2(e)'s (|t| 2^-27). Only elements with
+// e^(x - m) >= 1e-6 * sum (so t >= -20) can move the 1e-5 relative gate, whose denominator is
+// max(|r|, 1e-6): for them the numerator is within 20 (2^-23 + 2^-27) ln 2 + 2^-23 of e^(x - m),
+// about 1.9e-6 relative (measured: 8.8e-7 against binary64). It holds for any finite maximum;
+// padding (-inf) gives 0, and a row holding +inf or only -inf gives NaN, as the reference's
+// exp(x - max) does. (A libm expf and an IEEE divide per element cost twice the vector
+// instructions, which did not hide behind the row stream.)
 constexpr float kLog2eF = 1.44269502f;  // log2(e) rounded to binary32
-__device__ __forceinline__ float exp_row(float x, float mL) { return __builtin_amdgcn_exp2f(fmaf(x, kLog2eF, -mL)); }
-
-// e^d on v_exp_f32 with the rounding error of the product d * log2(e) (recovered exactly by an
-// fma) and the tail of log2(e) folded back in as 2^p * (1 + err * ln 2): at most 1.23 ulp against
-// binary64 over d in [-87.3, 0] (measured on the device); e^-inf = 0; NaN propagates. The softmax
-// of a row whose maximum is beyond exp_row's range.
-__device__ __forceinline__ float exp_softmax(float d) {
-  constexpr float kLog2eTail = 1.925963033e-8f;  // log2(e) - kLog2eF
-  constexpr float kLn2 = 0.693147181f;
-  const float p = d * kLog2eF;
-  const float err = fmaf(d, kLog2eTail, fmaf(d, kLog2eF, -p));
-  const float r = __builtin_amdgcn_exp2f(p);
-  return (r == 0.f) ? 0.f : fmaf(r, err * kLn2, r);
-}
+__device__ __forceinline__ float exp_sub(float x, float m) { return __builtin_amdgcn_exp2f((x - m) * kLog2eF); }
 
 // TPR threads own one row at a time and each keeps NV float4 of it in registers; a workgroup
 // walks RPB rows (RPB > 1: the next row's loads are issued before the current row's reduction,
 // so the reduction's latency hides behind HBM traffic). GS (one wavefront per row, RPB = 1): the
-// workgroup's four rows store together after one barrier, and the RMSNorm gain is staged in LDS
-// once per workgroup instead of read by every lane. At 4096 x 4096 RMSNorm runs 7% faster in this
-// form than in the two-row walk (and faster than a plain copy of one row per workgroup); in
-// standalone copies, the barrier before the stores and the gain in LDS each gained on their own.
-// Row-sum and softmax run slower in it. Rows beyond L are masked, never skipped: every thread
-// reaches every barrier.
+// workgroup's four rows store together after one barrier, and a gain vector (RMSNorm's W,
+// channelscale's S, softmax's unit gain) is staged in LDS once per workgroup, after the row's
+// loads, by a loop whose every load is waited for before the next is issued. That staging is
+// part of what makes the form fast, and not only for its gain reads: in standalone copies at
+// 4096 x 4096 the same softmax took 23.5 us without it and 21.8 us with it (a table of ones), and
+// neither one extra load, four loads under one wait, nor pauses of 0.25-4 us before or after the
+// compute reproduced the gain. RMSNorm runs 7% faster in this form than in the two-row walk (and
+// faster than a plain copy of one row per workgroup). Row-sum runs slower in it. Rows beyond L
+// are masked, never skipped: every thread reaches every barrier.
 template <int TPR, int NV, int OP, bool NT, int RPB, bool GS = false>
 __global__ void __launch_bounds__(TPR < 256 ? 256 : TPR)
     rows_kernel(const float* __restrict__ X, const float* __restrict__ Wg, float* __restrict__ Y, int L, int C,
@@ -86,8 +76,9 @@ __global__ void __launch_bounds__(TPR < 256 ? 256 : TPR)
   // k+1's partial while a slow one still reads row k's.
   __shared__ float red0[2][WG / 64];
   __shared__ float red1[2][WG / 64];
-  // OP 3 (channelscale) scales by S[c] the way RMSNorm applies its gain, with no row statistic.
-  constexpr bool kGain = OP == 1 || OP == 3;
+  // OP 3 (channelscale) scales by S[c] the way RMSNorm applies its gain, with no row statistic;
+  // softmax takes a gain in the grouped-store form only (the launcher passes ones: x * 1 is x).
+  constexpr bool kGain = OP == 1 || OP == 3 || (OP == 2 && GS);
   __shared__ f32x4 gain_lds[(kGain && GS) ? TPR * NV : 1];
 
   const int tid = threadIdx.x;
@@ -216,27 +207,14 @@ __global__ void __launch_bounds__(TPR < 256 ? 256 : TPR)
 #pragma unroll
       for (int i = 0; i < NV; ++i) m = fmaxf(m, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
       m = row_reduce_max(m, red0[k & 1]);
-      // A wavefront holds part of one row only (TPR >= 64), so m is uniform: branch on a scalar.
-      const float mL = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, m * kLog2eF)));
       float s = 0.f;
-      if (__builtin_fabsf(mL) < 0x1p24f) {
 #pragma unroll
-        for (int i = 0; i < NV; ++i) {
-          v[i].x = exp_row(v[i].x, mL);
-          v[i].y = exp_row(v[i].y, mL);
-          v[i].z = exp_row(v[i].z, mL);
-          v[i].w = exp_row(v[i].w, mL);
-          s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-          v[i].x = exp_softmax(v[i].x - m);
-          v[i].y = exp_softmax(v[i].y - m);
-          v[i].z = exp_softmax(v[i].z - m);
-          v[i].w = exp_softmax(v[i].w - m);
-          s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
-        }
+      for (int i = 0; i < NV; ++i) {
+        v[i].x = exp_sub(v[i].x, m);
+        v[i].y = exp_sub(v[i].y, m);
+        v[i].z = exp_sub(v[i].z, m);
+        v[i].w = exp_sub(v[i].w, m);
+        s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
       }
       s = row_reduce_sum(s, red1[k & 1]);
       // One correctly rounded reciprocal per row, then a multiply per element: within one
@@ -247,7 +225,15 @@ __global__ void __launch_bounds__(TPR < 256 ? 256 : TPR)
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
           const int j = i * TPR + t;
-          if (j < C4) st4<NT>(y4 + j, f32x4{v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv});
+          if (j < C4) {
+            if constexpr (GS) {
+              const f32x4 gi = gain_lds[j];
+              st4<NT>(y4 + j, f32x4{(v[i].x * inv) * gi.x, (v[i].y * inv) * gi.y, (v[i].z * inv) * gi.z,
+                                    (v[i].w * inv) * gi.w});
+            } else {
+              st4<NT>(y4 + j, f32x4{v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv});
+            }
+          }
         }
       }
     }
@@ -365,11 +351,40 @@ __global__ void __launch_bounds__(kReduceThreads)
   }
 }
 
+// The grouped-store softmax's gain: ones for the widest row the form holds (4096 floats).
+constexpr int kUnitGainFloats = 64 * 16 * 4;
+struct UnitGain {
+  float v[kUnitGainFloats];
+};
+constexpr UnitGain unit_gain_ones() {
+  UnitGain u{};
+  for (int i = 0; i < kUnitGainFloats; ++i) u.v[i] = 1.0f;
+  return u;
+}
+__device__ __align__(16) UnitGain unit_gain = unit_gain_ones();
+
 }  // namespace uk::kern
 
 namespace uk {
 
 namespace {
+// Device address of the unit gain on the current device, looked up once per device (the host
+// name of a __device__ variable is a stand-in, not its address).
+const float* unit_gain_device() {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static const float* addr[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lk(mu);
+  if (!addr[dev]) {
+    void* q = nullptr;
+    if (hipGetSymbolAddress(&q, HIP_SYMBOL(kern::unit_gain)) != hipSuccess) return nullptr;
+    addr[dev] = static_cast<const float*>(q);
+  }
+  return addr[dev];
+}
+
 template <int TPR, int NV, bool NT, int RPB, bool GS>
 hipError_t rows_dispatch_op(RowOp op, const float* X, const float* W, float* Y, int64_t L, int64_t C, float eps,
                             hipStream_t s) {
@@ -418,6 +433,10 @@ hipError_t launch_rows(const Plan& p, RowOp op, const float* X, const float* W, 
   }
   if (p.family != Family::Rows || p.variant < 0 || p.variant >= kNumRowsVariants) return hipErrorInvalidValue;
   const RowsVariant v = kRowsVariants[p.variant];
+  if (op == RowOp::Softmax && v.grp) {
+    W = unit_gain_device();
+    if (!W) return hipErrorInvalidSymbol;
+  }
   // The register-resident kernel reads float4 at row*C + 4j: rows must be 16-byte aligned and
   // the row must fit the variant's capacity.
   if ((C & 3) != 0 || C > (int64_t)v.tpr * v.nv * 4) return hipErrorInvalidValue;
