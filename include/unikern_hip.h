@@ -167,11 +167,11 @@ int uk_solve(const char* hcs_json, const uk_op_desc* d, uk_plan* out, char* log,
  *   softmax:       in[0]=X; out=Y               rmsnorm: in[0]=X, in[1]=W[C]; out=Y
  *   channelscale:  in[0]=X, in[1]=S[C]; out=Y
  * plan may be NULL (solved against the built-in MI355X description).
- * The 1-D reduce keeps its pass-1 partials in a library-owned buffer, one per (device, stream),
- * allocated on the first 1-D reduce enqueued on that stream (8 KiB); launches on one stream run
- * in order, so they never share partials with another stream. uk_stream_destroy frees its
- * stream's buffer; a stream created outside the library keeps its buffer until the process ends
- * (uk_launch_noalloc needs none). */
+ * Allocates nothing. The 1-D reduce keeps its pass-1 partials (8 KiB) in a static device array,
+ * one per GPU, held until the process ends; a 1-D reduce waits (hipStreamWaitEvent on one event
+ * per GPU) for the previous one enqueued on that GPU through uk_launch or uk_launch_n, whatever
+ * its stream, so two never share the partials at once. That wait is an event recorded outside
+ * any graph: callers under HIP graph capture use uk_launch_noalloc. */
 int uk_launch(const uk_op_desc* d, const uk_plan* plan, const void* const* in, int32_t n_in, void* out,
               void* stream);
 /* uk_launch that allocates nothing: no counterpart in the reference; for callers that cannot
@@ -294,7 +294,6 @@ int uk_memcpy_dtoh(void* dst, const void* src, size_t bytes);
 int uk_memset(void* p, int value, size_t bytes);
 int uk_synchronize(void);
 int uk_stream_create(void** stream);
-/* Synchronises the stream, frees the 1-D reduce partials uk_launch kept for it, destroys it. */
 int uk_stream_destroy(void* stream);
 int uk_stream_synchronize(void* stream);
 int uk_event_create(void** ev);

@@ -191,6 +191,30 @@ def test_reduce1d(gpu, n):
     assert abs(y - float(O.reduce_blocked(x))) <= 1e-5 * float(np.sum(np.abs(x.astype(np.float64))))
 
 
+def test_reduce1d_interleaved_on_two_streams(gpu):
+    # uk_launch's 1-D reduces share one partials array per GPU and are ordered through one event:
+    # reduces enqueued alternately on two streams, with no synchronisation between them, each
+    # give the result the same reduce gives alone.
+    xs = [O.normal(n, 41 + n, 0.0, 1.0) for n in (12_345_679, 4_000_037)]
+    d = [gpu.make_desc("reduce", [x.size]) for x in xs]
+    xb = [gpu.DeviceBuffer.from_array(x) for x in xs]
+    solo = []
+    for k in range(2):
+        yb = gpu.DeviceBuffer(4)
+        gpu.launch(d[k], [xb[k]], yb)
+        solo.append(yb.download(np.float32, (1,))[0])
+    outs = [[gpu.DeviceBuffer(4) for _ in range(6)] for _ in range(2)]
+    with gpu.Stream() as s0, gpu.Stream() as s1:
+        for i in range(6):
+            for k, st in enumerate((s0, s1)):
+                gpu.launch(d[k], [xb[k]], outs[k][i], stream=st.ptr, sync=False)
+        s0.synchronize()
+        s1.synchronize()
+    for k in range(2):
+        for yb in outs[k]:
+            assert yb.download(np.float32, (1,))[0].view(np.uint32) == solo[k].view(np.uint32)
+
+
 def test_reduce1d_reference_verify_instance(gpu):
     # The reference's own device verify (src/codegen_hip.cpp:916-941): 2^20 values of 2^-6 sum to
     # exactly 16384 in any binary32 order.

@@ -1,7 +1,8 @@
 """uk_launch_noalloc, the entry point that allocates nothing, against uk_launch through the C ABI.
 
-The two share their kernels; only the 1-D reduce needs scratch (its pass-1 partials), which
-uk_launch_noalloc takes from a static device array instead of a library allocation. Results must
+The two share their kernels; only the 1-D reduce needs scratch (its pass-1 partials), which each
+takes from a static device array of its own (uk_launch orders its reduces through an event,
+uk_launch_noalloc leaves ordering to the caller). Results must
 be bit-identical to uk_launch's, on two calls in a row with the second on a smaller input (the
 array keeps the first call's partials; nothing in it may leak into the second result).
 """

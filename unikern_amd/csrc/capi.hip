@@ -40,6 +40,11 @@ int fail(int code, const std::string& msg) {
   return code;
 }
 
+int hip_rc(hipError_t e, const char* what) {
+  if (e == hipSuccess) return UK_OK;
+  return fail(UK_HIP_FAILURE, std::string("UNIKERN_ERROR what=") + what + " msg=" + hipGetErrorString(e));
+}
+
 int put(const std::string& s, char* out, size_t cap) {
   if (!out || cap == 0) return int(s.size());
   const size_t n = std::min(s.size(), cap - 1);
@@ -191,31 +196,48 @@ size_t scratch_bytes(const KmlTree& t) {
   return t.op == OpKind::Reduction && t.ndims == 1 ? sizeof(float) * kReduceParts : 0;
 }
 
-// uk_launch's scratch: one buffer per (device, stream), allocated on the first launch on that
-// stream that needs one. Launches on one stream execute in order, so they never overlap on one
-// buffer; launches on different streams get different buffers. uk_stream_destroy synchronises
-// its stream and frees that stream's buffer before destroying it, so a handle the runtime
-// recycles starts without one. A stream created outside the library keeps its buffer (8 KiB)
-// until the process ends.
-std::mutex g_scratch_mu;
-std::map<std::pair<int, hipStream_t>, Scratch> g_stream_scratch;
+// uk_launch's scratch: the 1-D reduce's pass-1 partials in a file-scope device array of their
+// own, one copy per GPU, so uk_launch allocates nothing. Launches on one stream run in order;
+// launches on different streams are ordered through one event per GPU: each 1-D reduce waits for
+// the previous one's record, wherever it was enqueued, and records its own, so two 1-D reduces
+// never hold the partials at once. (uk_launch_noalloc's array is a different one.)
+static __device__ __align__(256) float launch_partials[kReduceParts];
 
-int stream_scratch(hipStream_t stream, size_t need, Scratch* out) {
-  if (need == 0) return UK_OK;
+struct PartialsSlot {
+  void* addr = nullptr;      // device address of launch_partials on this GPU
+  hipEvent_t last = nullptr;  // recorded after the latest 1-D reduce enqueued on this GPU
+  bool recorded = false;
+};
+std::mutex g_partials_mu;
+PartialsSlot g_partials[64];
+
+// Enqueues fn(scratch) on `stream`, with the current GPU's partials when the op needs scratch,
+// after every 1-D reduce enqueued earlier through this path on that GPU.
+template <class F>
+int with_launch_partials(const KmlTree& t, hipStream_t stream, F&& fn) {
+  if (scratch_bytes(t) == 0) return fn(Scratch{});
+  static_assert(sizeof(launch_partials) >= sizeof(float) * kReduceParts, "partials hold pass 1");
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return fail(UK_HIP_FAILURE, "UNIKERN_ERROR what=hipGetDevice");
-  std::lock_guard<std::mutex> lk(g_scratch_mu);
-  Scratch& slot = g_stream_scratch[{dev, stream}];
-  if (slot.bytes < need) {
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return fail(UK_HIP_FAILURE, "UNIKERN_ERROR what=hipGetDevice");
+  std::lock_guard<std::mutex> lk(g_partials_mu);
+  PartialsSlot& slot = g_partials[dev];
+  if (!slot.addr) {
     void* q = nullptr;
-    const hipError_t e = hipMalloc(&q, need);
-    if (e != hipSuccess)
-      return fail(UK_HIP_FAILURE, std::string("UNIKERN_ERROR what=scratch msg=") + hipGetErrorString(e));
-    if (slot.ptr) (void)hipFree(slot.ptr);  // only ever grows; the old one is idle (same stream)
-    slot = {q, need};
+    hipError_t e = hipGetSymbolAddress(&q, HIP_SYMBOL(launch_partials));
+    if (e == hipSuccess && !slot.last) e = hipEventCreateWithFlags(&slot.last, hipEventDisableTiming);
+    if (e != hipSuccess || !q)
+      return fail(UK_HIP_FAILURE, std::string("UNIKERN_ERROR what=partials msg=") + hipGetErrorString(e));
+    slot.addr = q;
   }
-  *out = slot;
-  return UK_OK;
+  if (slot.recorded) {
+    if (int rc = hip_rc(hipStreamWaitEvent(stream, slot.last, 0), "hipStreamWaitEvent")) return rc;
+  }
+  const int rc = fn(Scratch{slot.addr, sizeof(float) * kReduceParts});
+  // Recorded whatever fn returned: whatever it enqueued is ordered before the next 1-D reduce.
+  if (int rc2 = hip_rc(hipEventRecord(slot.last, stream), "hipEventRecord")) return rc ? rc : rc2;
+  slot.recorded = true;
+  return rc;
 }
 
 // Device address of `scratch` on the current device, looked up with that device current on the
@@ -1105,9 +1127,8 @@ int uk_launch(const uk_op_desc* d, const uk_plan* plan, const void* const* in, i
                                        std::to_string(n_inputs(t)) + " inputs and an output");
   for (int i = 0; i < n_inputs(t); ++i)
     if (!in[i]) return fail(UK_BAD_INVOCATION, "UNIKERN_ERROR what=bad_invocation reason=null input");
-  Scratch ws;
-  if (int rc = stream_scratch(static_cast<hipStream_t>(stream), scratch_bytes(t), &ws)) return rc;
-  return dispatch(t, p, in, out, static_cast<hipStream_t>(stream), ws);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  return with_launch_partials(t, st, [&](const Scratch& ws) { return dispatch(t, p, in, out, st, ws); });
 }
 
 int uk_launch_noalloc(const uk_op_desc* d, const uk_plan* plan, const void* const* in, int32_t n_in, void* out,
@@ -1139,14 +1160,14 @@ int uk_launch_n(const uk_op_desc* d, const uk_plan* plan, const void* const* in_
   if (device_ok(nullptr) != UK_OK) return fail(UK_HIP_FAILURE, "UNIKERN_ERROR what=device reason=not gfx950");
   if (!in_sets || !out_sets || n_sets <= 0 || iters < 0 || n_in < n_inputs(t))
     return fail(UK_BAD_INVOCATION, "UNIKERN_ERROR what=bad_invocation reason=bad set arguments");
-  Scratch ws;
-  if (int rc = stream_scratch(static_cast<hipStream_t>(stream), scratch_bytes(t), &ws)) return rc;
-  for (int32_t i = 0; i < iters; ++i) {
-    const int32_t s = i % n_sets;
-    if (int rc = dispatch(t, p, in_sets + size_t(s) * n_in, out_sets[s], static_cast<hipStream_t>(stream), ws))
-      return rc;
-  }
-  return UK_OK;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  return with_launch_partials(t, st, [&](const Scratch& ws) {
+    for (int32_t i = 0; i < iters; ++i) {
+      const int32_t s = i % n_sets;
+      if (int rc = dispatch(t, p, in_sets + size_t(s) * n_in, out_sets[s], st, ws)) return rc;
+    }
+    return int(UK_OK);
+  });
 }
 
 int uk_format_result(const uk_result* r, char* line, size_t cap) {
@@ -1625,10 +1646,6 @@ int uk_q8_0_pack(const int8_t* q, const uint16_t* dd, uint8_t* blocks, int32_t N
   return UK_OK;
 }
 
-static int hip_rc(hipError_t e, const char* what) {
-  if (e == hipSuccess) return UK_OK;
-  return fail(UK_HIP_FAILURE, std::string("UNIKERN_ERROR what=") + what + " msg=" + hipGetErrorString(e));
-}
 int uk_malloc(void** p, size_t bytes) { return hip_rc(hipMalloc(p, bytes ? bytes : 4), "hipMalloc"); }
 int uk_free(void* p) { return hip_rc(hipFree(p), "hipFree"); }
 int uk_memcpy_htod(void* dst, const void* src, size_t bytes) {
@@ -1643,21 +1660,7 @@ int uk_stream_create(void** s) {
   return hip_rc(hipStreamCreate(reinterpret_cast<hipStream_t*>(s)), "hipStreamCreate");
 }
 int uk_stream_destroy(void* s) {
-  const hipStream_t st = static_cast<hipStream_t>(s);
-  if (st) {
-    // Pending launches may still use the stream's scratch: let them finish, then free it.
-    if (int rc = hip_rc(hipStreamSynchronize(st), "hipStreamSynchronize")) return rc;
-    std::lock_guard<std::mutex> lk(g_scratch_mu);
-    for (auto it = g_stream_scratch.begin(); it != g_stream_scratch.end();) {
-      if (it->first.second == st) {
-        if (it->second.ptr) (void)hipFree(it->second.ptr);
-        it = g_stream_scratch.erase(it);
-      } else {
-        ++it;
-      }
-    }
-  }
-  return hip_rc(hipStreamDestroy(st), "hipStreamDestroy");
+  return hip_rc(hipStreamDestroy(static_cast<hipStream_t>(s)), "hipStreamDestroy");
 }
 int uk_stream_synchronize(void* s) {
   return hip_rc(hipStreamSynchronize(static_cast<hipStream_t>(s)), "hipStreamSynchronize");
