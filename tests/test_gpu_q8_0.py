@@ -53,25 +53,28 @@ def test_llama7b_decode_shapes(gpu, M, N):
     assert np.all(np.abs(y - r) <= 1e-5 * np.linalg.norm(r, axis=1, keepdims=True) / np.sqrt(N) * 10)
 
 
-def test_dequant_bit_exact_one_hot(gpu):
+@pytest.mark.parametrize("M", [16, 5, 1])
+def test_dequant_bit_exact_one_hot(gpu, M):
     # Row m of X is one-hot at column k_m: y[m][n] = d[n][k_m/32] * q[n][k_m] exactly, so the
-    # kernel's dequantisation and its block/lane indexing are checked value by value.
+    # kernel's dequantisation and its block/lane indexing are checked value by value. M = 16
+    # takes the whole-line activation loads, M = 5 and M = 1 the activations copied into LDS.
     N, K = 96, 512
     blocks, _, _ = make_weights(N, K, 77)
     deq = O.q8_0_dequant(blocks, N, K)
     for start in range(0, K, 16 * 7):
-        ks = [(start + 7 * j) % K for j in range(16)]
-        X = np.zeros((16, K), np.float32)
-        X[np.arange(16), ks] = 1.0
+        ks = [(start + 7 * j) % K for j in range(M)]
+        X = np.zeros((M, K), np.float32)
+        X[np.arange(M), ks] = 1.0
         y = q8_gpu(gpu, O.f16_bits(X), blocks, N)
         want = deq[:, ks].T
         assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
 
 
-def test_exact_arithmetic_bit_exact(gpu):
+@pytest.mark.parametrize("M", [16, 5, 1])
+def test_exact_arithmetic_bit_exact(gpu, M):
     # Power-of-two scales and small-integer activations: every product and partial sum is exact,
     # so the f32 result equals the binary64 oracle rounded once (i.e. exactly).
-    M, N, K = 16, 256, 1024
+    N, K = 256, 1024
     blocks, _, _ = make_weights(N, K, 0, exact=True)
     X = ((np.arange(M * K) % 5) - 2).astype(np.float32).reshape(M, K)
     y = q8_gpu(gpu, O.f16_bits(X), blocks, N)
@@ -88,11 +91,12 @@ def test_ragged_shapes(gpu, M, N, K):
 
 @pytest.mark.parametrize("vi", range(10))
 @pytest.mark.parametrize("K", [2048, 4608])
-@pytest.mark.parametrize("M", [8, 13])
+@pytest.mark.parametrize("M", [1, 5, 8, 13])
 def test_every_variant(gpu, vi, K, M):
     # K = 4608 (72 block pairs) leaves a partial last round for every variant; N = 300 leaves a
     # partial last weight tile for the 64-row workgroups. M = 13 takes the whole-line activation
-    # loads (M > 8) with rows 13-15 past M.
+    # loads (M > 8) with rows 13-15 past M; M = 1, 5 and 8 the activations copied into LDS where
+    # the variant has room for them (M = 5: the last copy's upper half masked).
     p = gpu.Plan()
     p.family, p.variant = 8, vi
     N = 300

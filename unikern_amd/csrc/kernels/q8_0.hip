@@ -73,6 +73,14 @@ __device__ __forceinline__ void q8_wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// XL (activations through LDS, one-round-at-a-time kernels of 4 pairs per wavefront, M <= 8): each
+// wavefront copies the 512-byte slices of its pairs of the XL real activation rows (XL = 1: row
+// 0; XL = 8: rows m0 .. M - 1) into LDS with 16-byte direct-to-LDS copies, one instruction per
+// two rows, and reads the operands from there (rows past M read row 0 as an LDS broadcast). The
+// register form issues 2 P loads per lane for the same bytes, and each 16-lane row group of
+// them requests the same addresses. Same bits either way; bench.py (rotating activation and
+// weight sets) on one box: N = K = 4096, M = 1 5.94 -> 5.67 us, M = 8 6.54 -> 6.47 us;
+// N = 11008, M = 1 12.00 -> 11.72 us (XL = 8 is used by the one-tile kernels only).
 // FL (whole lines, used for M > 8 in the one-tile kernels): the activation loads of a pair cover
 // whole 128-byte lines, rows 0-7 in one load (lanes i < 8: row i's even block, lanes i >= 8: row
 // i - 8's odd block, bytes 16 g of the block) and rows 8-15 in the other, and two masked DPP row
@@ -81,7 +89,7 @@ __device__ __forceinline__ void q8_wait_vmcnt() {
 // 1.7 times slower for the same bytes. Same load count per round either way. (A/B on one box at
 // M = 16: 2% faster at N = 4096 with one tile; 1% slower at N = 11008 with three, where each
 // rebuilt operand feeds three MFMA tiles and the moves are not worth it.)
-template <int WAVES, int P, int VEC, bool DB, int NT, bool FL>
+template <int WAVES, int P, int VEC, bool DB, int NT, bool FL, int XL = 0>
 __global__ void __launch_bounds__(WAVES * 64)
     q8_0_gemm_kernel(const _Float16* __restrict__ X, const uint8_t* __restrict__ Wq, float* __restrict__ Y, int M,
                      int N, int K) {
@@ -95,7 +103,10 @@ __global__ void __launch_bounds__(WAVES * 64)
   constexpr int kInst = (kUnits + 63) / 64;        // DMA instructions per round
   static_assert(2 * (2 * P + kInst) <= 63, "two rounds of loads must fit the vmcnt counter");
   static_assert(WAVES * kWaveDw >= WAVES * 256 * NT, "the partials fold reuses the staging buffer");
+  static_assert(XL == 0 || ((XL == 1 || XL == 8) && P == 4 && !DB && !FL),
+                "activation copies: 512-byte slices of 1 or up to 8 rows, each round waited for in full");
   __shared__ uint32_t wl[WAVES * kWaveDw * (DB ? 2 : 1)];
+  __shared__ __attribute__((aligned(16))) _Float16 xs[XL ? WAVES * XL * 64 * P : 8];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int i = lane & 15, g = lane >> 4;
@@ -142,7 +153,20 @@ __global__ void __launch_bounds__(WAVES * 64)
   // Round issue: the activations of this wavefront's pairs p0 .. p0 + P - 1 and the weight
   // copies into `buf`. Pairs past K/64 read pair 0 (valid memory) and are skipped below. Every
   // round issues the same 2 P + kInst loads, which the explicit vmcnt waits below count.
+  // XL: rows staged (the MFMA operand's rows past them take row 0's slice).
+  const int xr = XL == 1 ? 1 : (M - m0 < XL ? M - m0 : XL);
   auto issue_x = [&](int p0, f16x8 (&xa)[P], f16x8 (&xb)[P]) __attribute__((always_inline)) {
+    if constexpr (XL > 0) {
+      // Lanes 0-31 copy row 2t's slice, lanes 32-63 row 2t + 1's (16 bytes each, in order).
+      const int64_t po = 64 * (p0 < npairs ? p0 : 0) + (lane & 31) * 8;
+      for (int t = 0; 2 * t < xr; ++t) {
+        const int r = 2 * t + (lane >> 5);
+        if (r < xr)
+          __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(X + (int64_t)(m0 + r) * K + po),
+                                           (lds_void*)(xs + (wave * XL + 2 * t) * 64 * P), 16, 0, 0);
+      }
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < P; ++j) {
       const int p = p0 + j;
@@ -186,6 +210,12 @@ __global__ void __launch_bounds__(WAVES * 64)
       // rows past M, which are never stored, so no select is spent on them.
       f16x8 x0 = xa[j];
       f16x8 x1 = xb[j];
+      if constexpr (XL > 0) {
+        const int xrow_l = XL == 1 ? 0 : (i < xr ? i : 0);
+        const _Float16* xl = xs + (wave * XL + xrow_l) * 64 * P + 64 * j + 8 * g;
+        x0 = *reinterpret_cast<const f16x8*>(xl);
+        x1 = *reinterpret_cast<const f16x8*>(xl + 32);
+      }
       if constexpr (FL) {
         // Even-block operand: lanes 8-15 of each 16-lane row take rows 8-15's even blocks from
         // lanes 0-7 of the second load (row_shr:8); odd-block operand: lanes 0-7 take rows 0-7's
@@ -297,9 +327,36 @@ __global__ void __launch_bounds__(WAVES * 64)
 namespace uk {
 
 namespace {
+// LDS bytes of an instantiation: the weight staging plus the activation slices of XL rows.
+constexpr int q8_lds_bytes(int waves, int p, int vec, bool db, int nt, int xl) {
+  return waves * nt * 16 * 17 * p * 4 * (db ? 2 : 1) + (xl ? waves * xl * 64 * p * 2 : 16);
+}
+constexpr int kQ8LdsLimit = 160 * 1024;
+
 template <int WAVES, int P, int VEC, bool DB, int NT>
 hipError_t q8_go(const void* X, const void* Wq, float* Y, int64_t M, int64_t N, int64_t K, hipStream_t s) {
   const dim3 grid((unsigned)((N + 16 * NT - 1) / (16 * NT)), (unsigned)((M + 15) / 16));
+  // Activations through LDS at M <= 8 where the instantiation's LDS allows it.
+  if constexpr (P == 4 && !DB) {
+    if constexpr (q8_lds_bytes(WAVES, P, VEC, DB, NT, 1) <= kQ8LdsLimit) {
+      if (M == 1) {
+        hipLaunchKernelGGL((kern::q8_0_gemm_kernel<WAVES, P, VEC, DB, NT, false, 1>), grid, dim3(WAVES * 64), 0, s,
+                           static_cast<const _Float16*>(X), static_cast<const uint8_t*>(Wq), Y, (int)M, (int)N,
+                           (int)K);
+        return hipGetLastError();
+      }
+    }
+    // Eight rows only in the one-tile kernels: the three-tile kernel at N = 11008, M = 8 measured
+    // 12.83 us with them against 12.63 us without.
+    if constexpr (NT == 1 && q8_lds_bytes(WAVES, P, VEC, DB, NT, 8) <= kQ8LdsLimit) {
+      if (M <= 8) {
+        hipLaunchKernelGGL((kern::q8_0_gemm_kernel<WAVES, P, VEC, DB, NT, false, 8>), grid, dim3(WAVES * 64), 0, s,
+                           static_cast<const _Float16*>(X), static_cast<const uint8_t*>(Wq), Y, (int)M, (int)N,
+                           (int)K);
+        return hipGetLastError();
+      }
+    }
+  }
   // Whole-line activation loads in the one-tile kernels when more than 8 rows are real (at most
   // 8, the operand layout's half lines of the rows past M all fall on row 0).
   if constexpr (NT == 1) {
