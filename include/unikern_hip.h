@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define UK_ABI_VERSION 3
+#define UK_ABI_VERSION 4
 
 enum uk_status {
   UK_OK = 0,
@@ -78,6 +78,11 @@ typedef struct uk_plan {
   int32_t shard_rows; /* > 0: scenario B (reference src/codegen_hip.cpp:1143-1238): a GEMM whose
                          working set exceeds the device tier streams A and C in M-shards of this
                          many rows through pinned host buffers, B resident; 0: all resident */
+  int32_t stream_path; /* scenario B's data path for A (reference Instance::Path,
+                          include/unikern/core.hpp:70): 1 pinned copies (uk_stream_gemm), 2 mapped
+                          staging (uk_stream_gemm_file: A read from a file into host-mapped
+                          buffers that the kernel reads directly, src/codegen_hip.cpp:1239-1326);
+                          0 with shard_rows 0 */
   char key[64];     /* canonical candidate key */
 } uk_plan;
 
@@ -109,6 +114,9 @@ typedef struct uk_result {
   double cpu_ms;
   int32_t cpu_cores;
   int64_t cpu_outputs;
+  /* The data path a streamed run took, "pinned" or "mmap" (the reference's stream_path= token,
+   * src/codegen_hip.cpp:1716); empty for a resident run. */
+  char stream_path[8];
 } uk_result;
 
 /* ---- library / device ---- */
@@ -204,6 +212,17 @@ int uk_run(const char* hcs_json, const uk_op_desc* d, const uk_plan* plan, uint6
  * per call (the residency check applies to each). *pass_ms: the pass, first copy to last. */
 int uk_stream_gemm(const char* hcs_json, const uk_op_desc* d, const uk_plan* plan, const void* hA, const void* hB,
                    void* hC, double* pass_ms);
+/* Scenario B's mapped path (reference src/codegen_hip.cpp:1239-1326, uk_stream_pass_mmap): the
+ * same GEMM with A on disk. a_path names a file holding A [M][K] row-major in the GEMM's element
+ * type (f16 bits or f32), no header; hB and hC are host memory as for uk_stream_gemm. Per shard
+ * the host reads A's rows from the file into one of two host-mapped, coherent pinned staging
+ * buffers (the other still being read by the previous shard's kernel) and the kernel reads them
+ * through the mapped device pointer: no copy of A to the device runs, so A's bytes cross the link
+ * once per workgroup that consumes them, and A's host footprint is the two staging buffers. The
+ * shard height is plan->shard_rows as in uk_stream_gemm (plan NULL: solved against hcs_json).
+ * Refused (class 2) when the file is shorter than M K elements. *pass_ms: the pass. */
+int uk_stream_gemm_file(const char* hcs_json, const uk_op_desc* d, const uk_plan* plan, const char* a_path,
+                        const void* hB, void* hC, double* pass_ms);
 /* The UNIKERN_RESULT line for a result (reference src/codegen_hip.cpp:1710-1722 tokens + roofline). */
 int uk_format_result(const uk_result* r, char* line, size_t cap);
 /* Parse the output of one program run into a result (reference run_hip's parse,

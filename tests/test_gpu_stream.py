@@ -1,5 +1,6 @@
 """Scenario B on the device: the GEMM streamed in M-shards through pinned host memory (reference
-src/codegen_hip.cpp:1143-1238 uk_stream_pass, :1480-1708), with B resident.
+src/codegen_hip.cpp:1143-1238 uk_stream_pass, :1480-1708), with B resident, and its mapped path (A
+read from a file into host-mapped staging that the kernel reads, :1239-1326).
 
 On an MI355X (288 GB) no BASELINE GEMM exceeds the device tier, so these tests give the solver an
 HCS with a small device tier; the pass then really shards. Every output row is computed by the same
@@ -90,6 +91,56 @@ def test_run_streamed_mode_verifies(gpu):
     r = gpu.run(gpu.make_desc("gemm", [1024, 1024, 1024], dtype="fp16", layout="TN"), hcs_json=tier(6 << 20),
                 exact=True, iters=3)
     assert r.exit_code == 0 and r.verified and r.err_metric == 0 and "mode=streamed" in r.line, r.log
+
+
+def test_stream_file_f32_matches_resident_and_pinned(gpu, tmp_path):
+    # The mapped path (reference src/codegen_hip.cpp:1239-1326): A's shards are read from a file
+    # into host-mapped staging and the kernel reads them there. Same kernel, same k order: the
+    # result equals the resident launch's and the pinned stream's bit for bit.
+    M = N = K = 1024
+    d = gpu.make_desc("gemm", [M, N, K])
+    plan = gpu.solve(d, tier(12 << 20)).plan
+    assert plan.shard_rows > 0 and M // plan.shard_rows >= 2
+    A = O.uniform(M * K, 20261203, -1.0, 1.0).reshape(M, K)
+    B = O.uniform(K * N, 20261204, -1.0, 1.0).reshape(K, N)
+    path = tmp_path / "a_f32.bin"
+    A.tofile(path)
+    Cm, ms = gpu.stream_gemm_file(d, path, B, plan=plan)
+    assert ms > 0
+    Cp, _ = gpu.stream_gemm(d, A, B, plan=plan)
+    assert np.array_equal(Cm.view(np.uint32), Cp.view(np.uint32))
+    assert np.array_equal(Cm.view(np.uint32), resident_gemm(gpu, d, A, B, np.float32).view(np.uint32))
+
+
+@pytest.mark.parametrize("M,N,K,cap", [(3328, 2048, 1024, 24 << 20), (512, 768, 256, 1 << 30)])
+def test_stream_file_f16_matches_resident_bitwise(gpu, tmp_path, M, N, K, cap):
+    # (3328, ...) ends on a shorter shard; (512, ...) fits and runs as one shard. The file holds
+    # more than M K elements (a trailing row): only the first M K are read.
+    d = gpu.make_desc("gemm", [M, N, K], dtype="fp16", layout="TN")
+    plan = gpu.solve(d, tier(cap)).plan
+    A = O.f16_bits(O.uniform(M * K, 600 + M, -1.0, 1.0)).reshape(M, K)
+    B = O.f16_bits(O.uniform(N * K, 601 + N, -1.0, 1.0)).reshape(N, K)
+    path = tmp_path / "a_f16.bin"
+    np.concatenate([A, np.full((1, K), 0x7C00, np.uint16)]).tofile(path)
+    Cm, _ = gpu.stream_gemm_file(d, path, B, plan=plan if plan.shard_rows > 0 else None)
+    assert np.array_equal(Cm, resident_gemm(gpu, d, A, B, np.uint16))
+
+
+def test_run_streamed_mapped_path_verifies(gpu, monkeypatch):
+    # uk_run takes the plan's path unless UK_GEMM_STREAM_PATH pins one; the result line and the
+    # log say which ran and where the choice came from.
+    d = gpu.make_desc("gemm", [2048, 2048, 2048], dtype="fp16", layout="TN")
+    hcs = tier(24 << 20)
+    r = gpu.run(d, hcs_json=hcs, iters=3)
+    assert r.exit_code == 0 and r.verified and r.stream_path == "pinned", r.log
+    assert "stream_path=pinned source=plan plan=pinned" in r.log
+    monkeypatch.setenv("UK_GEMM_STREAM_PATH", "mmap")
+    r = gpu.run(d, hcs_json=hcs, iters=3)
+    assert r.exit_code == 0 and r.verified and r.stream_path == "mmap", r.log
+    assert "mode=streamed stream_path=mmap" in r.line and "stream_path=mmap source=env plan=pinned" in r.log
+    assert r.err_metric <= 1e-2 and r.measured_ms > 0 and r.kernel_ms > 0
+    r = gpu.run(gpu.make_desc("gemm", [1024, 1024, 1024]), hcs_json=tier(12 << 20), exact=True, iters=3)
+    assert r.exit_code == 0 and r.verified and r.err_metric == 0 and r.stream_path == "mmap", r.log
 
 
 def test_cli_streamed_run_commits_and_hits(gpu, tmp_path):

@@ -266,8 +266,16 @@ def test_streamed_plan_round_trips(uk, ledger_path):
         L.commit(GEMM, sol.plan, measured_ms=5.0, kernel_ms=0.2, hcs_json=hcs)
         hit = L.lookup(GEMM, hcs)
         assert hit.plan.shard_rows == sol.plan.shard_rows and hit.plan.key == sol.plan.key
+        assert hit.plan.stream_path == 1
         L.commit(ROWS, uk.solve(uk.kml_import(ROWS)).plan)
-        assert L.lookup(ROWS).plan.shard_rows == 0
+        assert L.lookup(ROWS).plan.shard_rows == 0 and L.lookup(ROWS).plan.stream_path == 0
+        # The mapped path is recorded through its plan key ("+stream_mmap"), so a hit runs it again.
+        mapped = sol.plan
+        mapped.stream_path = 2
+        mapped.key = sol.plan.key + b"_mmap"
+        L.commit(GEMM, mapped, measured_ms=9.0, kernel_ms=0.3, hcs_json=hcs)
+        hit = L.lookup(GEMM, hcs)
+        assert hit.plan.stream_path == 2 and hit.plan.key.endswith(b"+stream_mmap")
 
 
 def test_hcs_with_capacity(uk):

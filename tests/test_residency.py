@@ -10,6 +10,7 @@ import json
 import math
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 from test_cli import cli
@@ -156,6 +157,52 @@ def test_result_line_carries_cpu_tokens(uk):
     assert " cpu_ms=812.500 cpu_cores=16 cpu_outputs=131072" in r.line
 
 
+def test_result_line_carries_the_stream_path(uk):
+    # A streamed run names its data path after mode= (the reference's stream_path= token,
+    # src/codegen_hip.cpp:1716); a resident line has none and parses to "".
+    line = ("UNIKERN_RESULT backend=amd verify=PASS max_rel=0 measured_ms=90.0 kernel_ms=0.3 mode=streamed "
+            "stream_path=mmap payload_mb=96.0 perf=4096x4096x4096 dtype=fp16 migrations=0 checks=5")
+    r = uk.parse_result(line, 0)
+    assert r.stream_path == "mmap" and " mode=streamed stream_path=mmap payload_mb=" in r.line
+    assert uk.parse_result(r.line, 0).stream_path == "mmap"
+    r = uk.parse_result(line.replace("mode=streamed stream_path=mmap", "mode=resident"), 0)
+    assert r.stream_path == "" and "stream_path=" not in r.line
+
+
+def test_stream_path_pin_is_validated_before_the_device(uk, monkeypatch):
+    # UK_GEMM_STREAM_PATH pins scenario B's data path for A/B runs (pinned | mmap | auto); any
+    # other value is refused with class 2 before inputs or the device are touched, as the
+    # reference's program refuses it (src/codegen_hip.cpp:1344-1356).
+    g = uk.make_desc("gemm", [4096, 4096, 4096], dtype="fp16", layout="TN")
+    small = _tiny_hcs(96 << 20)
+    monkeypatch.setenv("UK_GEMM_STREAM_PATH", "zero-copy")
+    r = uk.run(g, hcs_json=small)
+    assert r.exit_code == uk.UK_BAD_INVOCATION and "UNIKERN_ERROR what=stream_path_pin_unfit val=zero-copy" in r.log
+    assert r.cpu_ms == -1.0  # refused before the inputs and their CPU pass
+    # A resident run does not stream, so the knob is not consulted.
+    assert "stream_path_pin_unfit" not in uk.run(uk.make_desc("gemm", [256, 256, 256], dtype="fp16", layout="TN"),
+                                                 hcs_json=small).log
+    for ok in ("pinned", "mmap", "auto"):
+        monkeypatch.setenv("UK_GEMM_STREAM_PATH", ok)
+        assert "stream_path_pin_unfit" not in uk.run(g, hcs_json=small).log
+
+
+def test_stream_gemm_file_refuses_a_short_or_missing_file(uk, tmp_path):
+    d = uk.make_desc("gemm", [64, 64, 64], dtype="fp16", layout="TN")
+    B = np.zeros((64, 64), np.uint16)
+    with pytest.raises(uk.UnikernError) as e:
+        uk.stream_gemm_file(d, tmp_path / "absent.bin", B)
+    assert e.value.code == uk.UK_BAD_INVOCATION and "mmap_open" in str(e.value)
+    short = tmp_path / "short.bin"
+    short.write_bytes(b"\0" * (64 * 64 * 2 - 2))
+    with pytest.raises(uk.UnikernError) as e:
+        uk.stream_gemm_file(d, short, B)
+    assert e.value.code == uk.UK_BAD_INVOCATION and "mmap_short_file need=8192 have=8190" in str(e.value)
+    with pytest.raises(uk.UnikernError) as e:
+        uk.stream_gemm_file(d, short, np.zeros((64, 64), np.float32))
+    assert e.value.code == uk.UK_BAD_INVOCATION and "stream_gemm_file:" in str(e.value)
+
+
 def test_parse_refusal_line(uk):
     # No result line: the oversubscription refusal still carries the rate's numerator and
     # denominator and the measured headroom (src/runner.cpp:199-214).
@@ -260,8 +307,6 @@ def test_cli_threshold_validated_at_parse(uk, tmp_path, bad):
 def test_stream_gemm_checks_operands_before_the_call(uk):
     # uk_stream_gemm copies rows straight out of the host arrays, so a short or mistyped array is
     # refused on the Python side before the library (or the device) is reached.
-    import numpy as np
-
     d = uk.make_desc("gemm", [256, 128, 64], dtype="fp16", layout="TN")
     A = np.zeros((256, 64), np.uint16)
     B = np.zeros((128, 64), np.uint16)

@@ -97,6 +97,39 @@ def test_streaming_plan_for_a_gemm_beyond_the_device_tier(uk):
     assert uk.solve(q, hcs(vram=56 << 20)).plan.shard_rows == 0
 
 
+def test_stream_data_paths_are_costed_candidates(uk):
+    # Scenario B's two paths for A (reference src/solver.cpp:14-44, :52-66, :96-121; its tests,
+    # tests/acceptance.cpp:1040-1090): pinned copies, and A read by the kernel from host-mapped
+    # staging paged in from storage. Without an nvme tier the mapped candidate is infeasible by a
+    # named predicate; with one it is costed and dominated (its copy term adds the nvme page-in
+    # and the link reads of every consuming workgroup column), so pinned is chosen by the cost
+    # model, even against an absurdly fast nvme tier.
+    g = uk.make_desc("gemm", [4096, 4096, 4096], dtype="fp16", layout="TN")
+    h = json.loads(hcs(vram=96 << 20))
+    plain = uk.solve(g, json.dumps(h))
+    assert plain.plan.stream_path == 1 and plain.key.endswith("+stream")
+    assert "violates mmap_stream_requires_nvme_tier_bw>0" in plain.log
+    assert "stream_path=mmap" not in plain.log
+    h["tiers"].append({"name": "nvme", "bytes": 2 << 40, "bw_gbps": 7, "confidence": "predicted"})
+    both = uk.solve(g, json.dumps(h))
+    assert both.plan.stream_path == 1 and both.key == plain.key
+    assert both.feasible == 2 * plain.feasible  # every kernel candidate with each path
+    cands = {ln.split()[1]: float(ln.split("predicted_us=")[1]) for ln in both.log.splitlines()
+             if ln.startswith("  candidate ") and "stream_path=" in ln}
+    pinned, mapped = cands[plain.key], cands[plain.key + "_mmap"]
+    assert mapped > pinned and pinned == pytest.approx(both.predicted_us, rel=1e-5)  # log prints 6 digits
+    # A at 7 GB/s once, and over the 64 GB/s link once per 256-column workgroup (16 of them),
+    # bound the mapped prediction from below.
+    a_bytes = 4096 * 4096 * 2
+    assert mapped >= a_bytes / 7e3 + a_bytes * 16 / 64e3
+    for t in h["tiers"]:
+        if t["name"] == "nvme":
+            t["bw_gbps"] = 100000
+    assert uk.solve(g, json.dumps(h)).plan.stream_path == 1
+    # Resident plans carry no data path.
+    assert uk.solve(g).plan.stream_path == 0
+
+
 def test_lds_predicate_filters_and_records(uk):
     small = hcs(lds_bytes_per_block=16384, lds_bytes_per_cu=16384)
     g = uk.solve(uk.make_desc("gemm", [4096, 4096, 4096], dtype="fp16", layout="TN"), small)

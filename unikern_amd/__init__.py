@@ -196,6 +196,7 @@ class RunOutcome:
     cpu_ms: float = -1.0      # the run's own CPU reference pass (binary64, over the outputs it checks)
     cpu_cores: int = -1       # host threads that pass ran on
     cpu_outputs: int = -1     # outputs it computed (all, or the sampled rows/images)
+    stream_path: str = ""     # a streamed run's data path for A: "pinned" or "mmap"
     raw: Result = field(repr=False, default=None)
 
 
@@ -215,7 +216,8 @@ def _outcome(r: Result, rc: int, log: str) -> RunOutcome:
     return RunOutcome(bool(r.built), bool(r.ran), bool(r.verified), rc, r.max_rel, r.err_metric, r.tol, r.kernel_ms,
                       r.measured_ms, r.achieved, r.peak, r.frac, "mfma" if r.bound == 1 else "hbm", r.migrations,
                       r.checks, r.vram_free, r.vram_total, r.plan.key.decode(), FAMILIES.get(r.plan.family, "?"),
-                      r.sets, log, line.value.decode(), r.cpu_ms, r.cpu_cores, r.cpu_outputs, r)
+                      r.sets, log, line.value.decode(), r.cpu_ms, r.cpu_cores, r.cpu_outputs,
+                      r.stream_path.decode(), r)
 
 
 def parse_result(program_output: str, exit_code: int) -> RunOutcome:
@@ -353,6 +355,31 @@ def stream_gemm(d: OpDesc, A: np.ndarray, B: np.ndarray, plan: Plan | None = Non
     _check(lib.uk_stream_gemm(None if hcs_json is None else _text(hcs_json), C.byref(d),
                               None if plan is None else C.byref(plan), A.ctypes.data_as(C.c_void_p),
                               B.ctypes.data_as(C.c_void_p), Cm.ctypes.data_as(C.c_void_p), C.byref(ms)))
+    return Cm, ms.value
+
+
+def stream_gemm_file(d: OpDesc, a_path: str | Path, B: np.ndarray, plan: Plan | None = None,
+                     hcs_json: str | None = None) -> tuple[np.ndarray, float]:
+    """Scenario B's mapped path (uk_stream_gemm_file): (C, pass_ms) with A [M][K] read from the file
+    at a_path (raw elements of the descriptor's dtype, row-major) shard by shard into host-mapped
+    staging that the kernel reads directly; B as for stream_gemm. The library refuses a file
+    shorter than M K elements."""
+    if d.op != OPS["gemm"] or d.ndims != 3:
+        raise UnikernError(UK_BAD_INVOCATION, "stream_gemm_file: the descriptor is not a gemm [M, N, K]")
+    M, N, K = (int(d.dims[i]) for i in range(3))
+    want = {DTYPES["fp16"]: np.uint16, DTYPES["fp32"]: np.float32}.get(int(d.dtype))
+    if want is None:
+        raise UnikernError(UK_BAD_INVOCATION, "stream_gemm_file: only fp16 and fp32 GEMMs stream")
+    b_shape = (N, K) if d.layout == LAYOUTS["TN"] else (K, N)
+    if B.dtype != want or tuple(B.shape) != b_shape:
+        raise UnikernError(UK_BAD_INVOCATION, f"stream_gemm_file: B is {B.dtype}{tuple(B.shape)}, the descriptor "
+                                              f"needs {np.dtype(want)}{b_shape}")
+    B = np.ascontiguousarray(B)
+    Cm = np.empty((M, N), dtype=want)
+    ms = C.c_double()
+    _check(lib.uk_stream_gemm_file(None if hcs_json is None else _text(hcs_json), C.byref(d),
+                                   None if plan is None else C.byref(plan), str(a_path).encode(),
+                                   B.ctypes.data_as(C.c_void_p), Cm.ctypes.data_as(C.c_void_p), C.byref(ms)))
     return Cm, ms.value
 
 

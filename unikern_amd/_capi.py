@@ -8,6 +8,7 @@ import ctypes as C
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libunikern_hip.so"
+ABI_VERSION = 4  # UK_ABI_VERSION of the header these declarations mirror
 
 UK_OK, UK_VERIFY_FAIL, UK_BAD_INVOCATION, UK_INFEASIBLE, UK_HIP_FAILURE, UK_RESIDENCY = range(6)
 OPS = {"gemm": 0, "conv": 1, "reduce": 2, "softmax": 3, "rmsnorm": 4, "channelscale": 5}
@@ -28,7 +29,7 @@ class Plan(C.Structure):
     _fields_ = [("family", C.c_int32), ("variant", C.c_int32), ("tile_m", C.c_int32), ("tile_n", C.c_int32),
                 ("tile_k", C.c_int32), ("threads", C.c_int32), ("tpr", C.c_int32), ("vec", C.c_int32),
                 ("split_k", C.c_int32), ("stages", C.c_int32), ("grid", C.c_int64), ("predicted_us", C.c_double),
-                ("feasible", C.c_int32), ("shard_rows", C.c_int32), ("key", C.c_char * 64)]
+                ("feasible", C.c_int32), ("shard_rows", C.c_int32), ("stream_path", C.c_int32), ("key", C.c_char * 64)]
 
 
 class Result(C.Structure):
@@ -40,7 +41,8 @@ class Result(C.Structure):
                 ("algo_bytes", C.c_int64), ("algo_flops", C.c_int64), ("weight_bytes", C.c_int64),
                 ("launches", C.c_int32), ("repeats", C.c_int32), ("sets", C.c_int32), ("plan", Plan),
                 ("mode", C.c_char * 16), ("dtype", C.c_char * 8), ("perf", C.c_char * 48),
-                ("cpu_ms", C.c_double), ("cpu_cores", C.c_int32), ("cpu_outputs", C.c_int64)]
+                ("cpu_ms", C.c_double), ("cpu_cores", C.c_int32), ("cpu_outputs", C.c_int64),
+                ("stream_path", C.c_char * 8)]
 
 
 class MfmaProbe(C.Structure):
@@ -74,6 +76,8 @@ _SIG = {
                 C.c_char_p, C.c_size_t], C.c_int),
     "uk_format_result": ([C.POINTER(Result), C.c_char_p, C.c_size_t], C.c_int),
     "uk_stream_gemm": ([C.c_char_p, C.POINTER(OpDesc), C.POINTER(Plan), _P, _P, _P, C.POINTER(C.c_double)], C.c_int),
+    "uk_stream_gemm_file": ([C.c_char_p, C.POINTER(OpDesc), C.POINTER(Plan), C.c_char_p, _P, _P,
+                             C.POINTER(C.c_double)], C.c_int),
     "uk_parse_result": ([C.c_char_p, C.c_int32, C.POINTER(Result)], C.c_int),
     "uk_migration_alarm": ([C.c_int32, C.c_int32, C.c_double, C.POINTER(C.c_double)], C.c_int),
     "uk_residency_class": ([C.c_int32, C.c_int32], C.c_int),
@@ -134,4 +138,7 @@ def load(path: Path | str = LIB_PATH) -> C.CDLL:
         fn = getattr(lib, name)
         fn.argtypes = args
         fn.restype = res
+    if lib.uk_abi_version() != ABI_VERSION:
+        raise ImportError(f"{p} reports ABI {lib.uk_abi_version()}, these declarations are ABI {ABI_VERSION}: "
+                          "rebuild it with `python3 unikern_amd/build.py`")
     return lib

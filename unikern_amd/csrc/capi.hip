@@ -8,6 +8,13 @@
 // (src/runner.cpp:146-238), since the kernels are compiled ahead of time.
 #include <hip/hip_runtime.h>
 
+#include <fcntl.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <cerrno>
+#include <cstdlib>
+
 #include <algorithm>
 #include <chrono>
 #include <cinttypes>
@@ -124,6 +131,7 @@ void plan_to_c(const Plan& p, uk_plan* o) {
   o->predicted_us = p.predicted_us;
   o->feasible = p.feasible;
   o->shard_rows = p.shard_rows;
+  o->stream_path = p.shard_rows > 0 ? (p.stream_path == 2 ? 2 : 1) : 0;
   std::snprintf(o->key, sizeof o->key, "%s", p.key.c_str());
 }
 
@@ -143,6 +151,7 @@ Plan plan_from_c(const uk_plan& c) {
   p.predicted_us = c.predicted_us;
   p.feasible = c.feasible;
   p.shard_rows = c.shard_rows;
+  p.stream_path = c.shard_rows > 0 ? (c.stream_path == 2 ? 2 : 1) : 0;
   p.key = std::string(c.key, strnlen(c.key, sizeof c.key));
   return p;
 }
@@ -419,16 +428,38 @@ struct DevArena {
 // copies of one shard overlap the kernel of the other. The host stages A rows into one of two
 // pinned buffers (refilled once the previous upload from it has completed) and drains C from one
 // of two pinned buffers (once its download has completed).
+// The mapped path (path 2, reference src/codegen_hip.cpp:1239-1326) reads A's shards from a file
+// into two host-mapped, coherent pinned staging buffers instead, and the kernel of a shard reads A
+// through the mapped device address: no copy of A to the device runs. The host refills a staging
+// buffer once the kernel that last read it (two shards earlier) has completed, while the kernel
+// of the shard in between runs.
 // ---------------------------------------------------------------------------------------
+
+// Reads n bytes at offset off of fd into dst (pread, retried over short reads); false on an
+// error or end of file before n bytes.
+bool read_at(int fd, char* dst, size_t n, int64_t off) {
+  size_t done = 0;
+  while (done < n) {
+    const ssize_t r = ::pread(fd, dst + done, n - done, off_t(off + int64_t(done)));
+    if (r < 0 && errno == EINTR) continue;
+    if (r <= 0) return false;
+    done += size_t(r);
+  }
+  return true;
+}
+
 struct StreamGemm {
   KmlTree t;        // the whole GEMM (dims[0] = M)
   Plan p;           // kernel variant and shard_rows
+  int path = 1;     // 1: A copied through pinned buffers; 2: A read by the kernel from mapped staging
   int64_t M = 0, N = 0, K = 0, es = 0, rows = 0, shards = 0;
   void* dB = nullptr;
   void* dA[2] = {nullptr, nullptr};
   void* dC[2] = {nullptr, nullptr};
   char* pinA[2] = {nullptr, nullptr};
   char* pinC[2] = {nullptr, nullptr};
+  char* stag[2] = {nullptr, nullptr};  // path 2: host-mapped staging for A's shards
+  void* dstag[2] = {nullptr, nullptr}; // their device addresses
   hipStream_t st[2] = {nullptr, nullptr};
   hipEvent_t a_done[2] = {nullptr, nullptr}, c_done[2] = {nullptr, nullptr};
   hipEvent_t b_ready = nullptr, start = nullptr, end[2] = {nullptr, nullptr};
@@ -444,9 +475,10 @@ struct StreamGemm {
   }
 
   // Device buffers from the caller's arena (residency-checked), pinned host buffers, streams.
-  int setup(const KmlTree& tree, const Plan& plan, DevArena& arena) {
+  int setup(const KmlTree& tree, const Plan& plan, DevArena& arena, int data_path = 1) {
     t = tree;
     p = plan;
+    path = data_path == 2 ? 2 : 1;
     const Shape sh = shape_of(t);
     M = sh.M;
     N = sh.N;
@@ -461,11 +493,21 @@ struct StreamGemm {
     const size_t a_bytes = size_t(rows * K * es), c_bytes = size_t(rows * N * es), b_bytes = size_t(K * N * es);
     if (int rc = arena.alloc(&dB, b_bytes, "stream_B")) return err = arena.err, rc;
     for (int b = 0; b < 2; ++b) {
-      if (int rc = arena.alloc(&dA[b], a_bytes, "stream_A")) return err = arena.err, rc;
-      if (int rc = arena.alloc(&dC[b], c_bytes, "stream_C")) return err = arena.err, rc;
       hipError_t e;
-      if ((e = hipHostMalloc(reinterpret_cast<void**>(&pinA[b]), a_bytes, hipHostMallocDefault)) != hipSuccess)
-        return fail_hip(e, "hipHostMalloc stream_A");
+      if (path == 2) {
+        // Coherent: the host refills these between kernels, so the device must not keep lines of
+        // them in its caches.
+        if ((e = hipHostMalloc(reinterpret_cast<void**>(&stag[b]), a_bytes,
+                               hipHostMallocMapped | hipHostMallocCoherent)) != hipSuccess)
+          return fail_hip(e, "hipHostMalloc stream_A_mapped");
+        if ((e = hipHostGetDevicePointer(&dstag[b], stag[b], 0)) != hipSuccess)
+          return fail_hip(e, "hipHostGetDevicePointer stream_A_mapped");
+      } else {
+        if (int rc = arena.alloc(&dA[b], a_bytes, "stream_A")) return err = arena.err, rc;
+        if ((e = hipHostMalloc(reinterpret_cast<void**>(&pinA[b]), a_bytes, hipHostMallocDefault)) != hipSuccess)
+          return fail_hip(e, "hipHostMalloc stream_A");
+      }
+      if (int rc = arena.alloc(&dC[b], c_bytes, "stream_C")) return err = arena.err, rc;
       if ((e = hipHostMalloc(reinterpret_cast<void**>(&pinC[b]), c_bytes, hipHostMallocDefault)) != hipSuccess)
         return fail_hip(e, "hipHostMalloc stream_C");
       if ((e = hipStreamCreate(&st[b])) != hipSuccess) return fail_hip(e, "hipStreamCreate");
@@ -490,17 +532,19 @@ struct StreamGemm {
       if (st[b]) (void)hipStreamDestroy(st[b]);
       if (pinA[b]) (void)hipHostFree(pinA[b]);
       if (pinC[b]) (void)hipHostFree(pinC[b]);
+      if (stag[b]) (void)hipHostFree(stag[b]);
     }
     if (b_ready) (void)hipEventDestroy(b_ready);
     if (start) (void)hipEventDestroy(start);
   }
 
-  // Kernel of shard s on stream st[s % 2]; the shard is the GEMM with M = its rows.
+  // Kernel of shard s on stream st[s % 2]; the shard is the GEMM with M = its rows. A comes from
+  // the shard's device buffer (path 1) or its mapped staging buffer (path 2).
   int kernel(int64_t s) {
     KmlTree ts = t;
     ts.dims[0] = int(rows_of(s));
     const int b = int(s & 1);
-    const void* in[2] = {dA[b], dB};
+    const void* in[2] = {path == 2 ? dstag[b] : dA[b], dB};
     return dispatch(ts, p, in, dC[b], st[b], ws);
   }
 
@@ -563,8 +607,66 @@ struct StreamGemm {
     return UK_OK;
   }
 
-  // Kernel-only time of one pass's shards on resident buffers (every shard's kernel, back to
-  // back on one stream, median over repeats), the reference's kernel-only figure for this path.
+  // One pass of the mapped path: A's rows from fd (A [M][K] from offset 0), hB and hC on the host.
+  int pass_file(int fd, const void* hB, void* hC, double* pass_ms) {
+    char* Cc = static_cast<char*>(hC);
+    const size_t arow = size_t(K * es), crow = size_t(N * es);
+    hipError_t e;
+    if ((e = hipEventRecord(start, st[0])) != hipSuccess) return fail_hip(e, "record start");
+    if ((e = hipStreamWaitEvent(st[1], start, 0)) != hipSuccess) return fail_hip(e, "wait start");
+    if ((e = hipMemcpyAsync(dB, hB, size_t(K * N * es), hipMemcpyHostToDevice, st[0])) != hipSuccess)
+      return fail_hip(e, "stream h2d B");
+    if ((e = hipEventRecord(b_ready, st[0])) != hipSuccess) return fail_hip(e, "record b_ready");
+    if ((e = hipStreamWaitEvent(st[1], b_ready, 0)) != hipSuccess) return fail_hip(e, "wait b_ready");
+    auto refill = [&](int64_t s) -> int {
+      const int b = int(s & 1);
+      // a_done[b]: the kernel of shard s - 2, the last reader of stag[b], has completed.
+      if (s >= 2 && (e = hipEventSynchronize(a_done[b])) != hipSuccess) return fail_hip(e, "wait a_done");
+      if (!read_at(fd, stag[b], size_t(rows_of(s)) * arow, int64_t(s * rows) * int64_t(arow))) {
+        err = "UNIKERN_ERROR what=mmap_read shard=" + std::to_string(s) + " msg=" + std::strerror(errno);
+        return UK_HIP_FAILURE;
+      }
+      return UK_OK;
+    };
+    auto drain = [&](int64_t s) -> int {
+      const int b = int(s & 1);
+      if ((e = hipEventSynchronize(c_done[b])) != hipSuccess) return fail_hip(e, "wait c_done");
+      std::memcpy(Cc + size_t(s * rows) * crow, pinC[b], size_t(rows_of(s)) * crow);
+      return UK_OK;
+    };
+    if (int rc = refill(0)) return rc;
+    for (int64_t s = 0; s < shards; ++s) {
+      const int b = int(s & 1);
+      if (int rc = kernel(s)) return err = g_err, rc;
+      if ((e = hipEventRecord(a_done[b], st[b])) != hipSuccess) return fail_hip(e, "record a_done");
+      if (s >= 2)
+        if (int rc = drain(s - 2)) return rc;
+      if ((e = hipMemcpyAsync(pinC[b], dC[b], size_t(rows_of(s)) * crow, hipMemcpyDeviceToHost, st[b])) !=
+          hipSuccess)
+        return fail_hip(e, "stream d2h shard");
+      if ((e = hipEventRecord(c_done[b], st[b])) != hipSuccess) return fail_hip(e, "record c_done");
+      // The next shard's rows go into the other buffer while this shard's kernel runs.
+      if (s + 1 < shards)
+        if (int rc = refill(s + 1)) return rc;
+    }
+    for (int64_t s = std::max<int64_t>(0, shards - 2); s < shards; ++s)
+      if (int rc = drain(s)) return rc;
+    double ms = 0;
+    for (int b = 0; b < 2; ++b) {
+      if ((e = hipEventRecord(end[b], st[b])) != hipSuccess) return fail_hip(e, "record end");
+      if ((e = hipEventSynchronize(end[b])) != hipSuccess) return fail_hip(e, "sync end");
+      float f = 0;
+      if ((e = hipEventElapsedTime(&f, start, end[b])) != hipSuccess) return fail_hip(e, "elapsed");
+      ms = std::max(ms, double(f));
+    }
+    if (pass_ms) *pass_ms = ms;
+    return UK_OK;
+  }
+
+  // Kernel-only time of one pass's shards (every shard's kernel, back to back on one stream,
+  // median over repeats), the reference's kernel-only figure for each path: on resident buffers
+  // for path 1, reading the first mapped staging buffer for path 2 (GEMM time does not depend
+  // on the values).
   int kernel_time(int repeats, double* ms_out) {
     hipError_t e;
     std::vector<double> per;
@@ -573,7 +675,7 @@ struct StreamGemm {
       for (int64_t s = 0; s < shards; ++s) {
         KmlTree ts = t;
         ts.dims[0] = int(rows_of(s));
-        const void* in[2] = {dA[0], dB};
+        const void* in[2] = {path == 2 ? dstag[0] : dA[0], dB};
         if (int rc = dispatch(ts, p, in, dC[0], st[0], ws)) return err = g_err, rc;
       }
       if ((e = hipEventRecord(k1[0], st[0])) != hipSuccess) return fail_hip(e, "record k1");
@@ -1175,13 +1277,15 @@ int uk_format_result(const uk_result* r, char* line, size_t cap) {
   char b[1024];
   const char* unit = r->bound == 1 ? "TFLOP/s" : "GB/s";
   const char* tk[] = {"max_rel", "rowsum_abs", "frobenius", "bit_exact_mismatches"};
+  // stream_path= follows mode= for a streamed run only (the reference prints it after mode=).
+  const bool sp = r->stream_path[0] != 0;
   std::snprintf(b, sizeof b,
-                "UNIKERN_RESULT backend=amd verify=%s max_rel=%.6e measured_ms=%.6f kernel_ms=%.6f mode=%s "
+                "UNIKERN_RESULT backend=amd verify=%s max_rel=%.6e measured_ms=%.6f kernel_ms=%.6f mode=%s%s%.8s "
                 "payload_mb=%.6f perf=%s dtype=%s migrations=%d checks=%d vram_free=%" PRIu64 " vram_total=%" PRIu64
                 " gate=%s err=%.6e tol=%.6e achieved=%.3f unit=%s peak=%.1f frac=%.4f plan=%s cpu_ms=%.3f cpu_cores=%d"
                 " cpu_outputs=%" PRId64,
                 r->verified ? "PASS" : "FAIL", r->max_rel, r->measured_ms, r->kernel_ms, r->mode,
-                double(r->algo_bytes) / (1024.0 * 1024.0), r->perf, r->dtype, r->migrations, r->checks, r->vram_free,
+                sp ? " stream_path=" : "", sp ? r->stream_path : "", double(r->algo_bytes) / (1024.0 * 1024.0), r->perf, r->dtype, r->migrations, r->checks, r->vram_free,
                 r->vram_total, tk[std::min(std::max(r->tol_kind, 0), 3)], r->err_metric, r->tol, r->achieved, unit,
                 r->peak, r->frac, r->plan.key, r->cpu_ms, r->cpu_cores, r->cpu_outputs);
   return put(b, line, cap);
@@ -1243,6 +1347,7 @@ int uk_parse_result(const char* program_output, int32_t exit_code, uk_result* ou
   out->frac = std::atof(token(line, "frac").c_str());
   out->bound = token(line, "unit") == "TFLOP/s" ? 1 : 0;
   std::snprintf(out->mode, sizeof out->mode, "%s", token(line, "mode").c_str());
+  std::snprintf(out->stream_path, sizeof out->stream_path, "%s", token(line, "stream_path").c_str());
   std::snprintf(out->dtype, sizeof out->dtype, "%s", token(line, "dtype").c_str());
   std::snprintf(out->perf, sizeof out->perf, "%s", token(line, "perf").c_str());
   std::snprintf(out->plan.key, sizeof out->plan.key, "%s", token(line, "plan").c_str());
@@ -1318,9 +1423,27 @@ int uk_run(const char* hcs_json, const uk_op_desc* d, const uk_plan* plan, uint6
     g_err = "UNIKERN_ERROR what=bad_invocation reason=only an f16 or f32 GEMM streams (shard_rows > 0)";
     return finish(UK_BAD_INVOCATION);
   }
+  // Scenario B's data path: the plan's, or UK_GEMM_STREAM_PATH (pinned | mmap | auto) for A/B
+  // runs (reference src/codegen_hip.cpp:1338-1356); whichever runs is reported as stream_path=.
+  int stream_path = streamed ? (p.stream_path == 2 ? 2 : 1) : 0;
+  const char* stream_src = "plan";
+  if (const char* pin = std::getenv("UK_GEMM_STREAM_PATH"); streamed && pin && *pin) {
+    if (std::strcmp(pin, "pinned") == 0) {
+      stream_path = 1;
+      stream_src = "env";
+    } else if (std::strcmp(pin, "mmap") == 0) {
+      stream_path = 2;
+      stream_src = "env";
+    } else if (std::strcmp(pin, "auto") != 0) {
+      g_err = std::string("UNIKERN_ERROR what=stream_path_pin_unfit val=") + pin;
+      return finish(UK_BAD_INVOCATION);
+    }
+  }
   const int64_t es = t.dtype == DType::F16 ? 2 : 4;
+  // The mapped path keeps no A on the device (its shards are read from host-mapped staging).
+  const int64_t shard_h = std::min<int64_t>(p.shard_rows, s.M);
   const int64_t device_bytes =
-      streamed ? s.K * s.N * es + 2 * std::min<int64_t>(p.shard_rows, s.M) * (s.K + s.N) * es : w.bytes;
+      streamed ? s.K * s.N * es + 2 * shard_h * ((stream_path == 2 ? 0 : s.K) + s.N) * es : w.bytes;
   if (double(device_bytes) > 0.85 * vram) {
     g_err = std::string("UNIKERN_ERROR what=stream_refused ") + (streamed ? "device_bytes=" : "payload_bytes=") +
             std::to_string(device_bytes) + " vram_bytes=" + std::to_string((long long)vram);
@@ -1359,9 +1482,10 @@ int uk_run(const char* hcs_json, const uk_op_desc* d, const uk_plan* plan, uint6
     // Scenario B (reference src/codegen_hip.cpp:1480-1708): verify one streamed pass, time
     // passes end to end (measured_ms) and the shards' kernels on resident buffers (kernel_ms).
     std::snprintf(out->mode, sizeof out->mode, "streamed");
+    std::snprintf(out->stream_path, sizeof out->stream_path, "%s", stream_path == 2 ? "mmap" : "pinned");
     DevArena arena;
     StreamGemm sg;
-    const int src = sg.setup(t, p, arena);
+    const int src = sg.setup(t, p, arena, stream_path);
     out->migrations = arena.migrations;
     out->checks = arena.checks;
     out->vram_free = arena.vram_free;
@@ -1371,10 +1495,45 @@ int uk_run(const char* hcs_json, const uk_op_desc* d, const uk_plan* plan, uint6
       return finish(src);
     }
     lg << "UNIKERN_INFO mode=streamed shards=" << sg.shards << " shard_rows=" << sg.rows
-       << " prefetch_d=2 stream_path=pinned\n";
+       << " prefetch_d=2 stream_path=" << out->stream_path << " source=" << stream_src
+       << " plan=" << (p.stream_path == 2 ? "mmap" : "pinned") << "\n";
+    // The mapped path reads A from storage: the generated A goes to a temporary file first
+    // (removed when the run ends), as the reference's program writes uk_gemm_streamA.bin.
+    struct TempFile {
+      std::string path;
+      int fd = -1;
+      ~TempFile() {
+        if (fd >= 0) ::close(fd);
+        if (!path.empty()) ::unlink(path.c_str());
+      }
+    } a_file;
+    if (stream_path == 2) {
+      const char* dir = std::getenv("TMPDIR");
+      std::string tpl = std::string(dir && *dir ? dir : "/tmp") + "/unikern_streamA_XXXXXX";
+      a_file.fd = ::mkstemp(tpl.data());
+      if (a_file.fd < 0) {
+        g_err = std::string("UNIKERN_ERROR what=mmap_file msg=") + std::strerror(errno);
+        return finish(UK_HIP_FAILURE);
+      }
+      a_file.path = tpl;
+      const auto& A = rd.ins[0].bytes;
+      for (size_t done = 0; done < A.size();) {
+        const ssize_t wr = ::write(a_file.fd, A.data() + done, A.size() - done);
+        if (wr < 0 && errno == EINTR) continue;
+        if (wr <= 0) {
+          g_err = std::string("UNIKERN_ERROR what=mmap_file_write msg=") + std::strerror(errno);
+          return finish(UK_HIP_FAILURE);
+        }
+        done += size_t(wr);
+      }
+    }
+    auto one_pass = [&](std::vector<uint8_t>& dst, double* ms) {
+      return stream_path == 2 ? sg.pass_file(a_file.fd, rd.ins[1].bytes.data(), dst.data(), ms)
+                              : sg.pass(rd.ins[0].bytes.data(), rd.ins[1].bytes.data(), dst.data(), ms);
+    };
     std::vector<uint8_t> host_out(rd.out_bytes, 0xFF);
     double pass_ms = 0;
-    if (int rc = sg.pass(rd.ins[0].bytes.data(), rd.ins[1].bytes.data(), host_out.data(), &pass_ms)) {
+    if (int rc = one_pass(host_out, &pass_ms)) {
       g_err = sg.err;
       return finish(rc);
     }
@@ -1388,7 +1547,7 @@ int uk_run(const char* hcs_json, const uk_op_desc* d, const uk_plan* plan, uint6
     out->tol_kind = rd.tol_kind;
     std::vector<double> passes;
     for (int r = 0; r < 3; ++r) {
-      if (int rc = sg.pass(rd.ins[0].bytes.data(), rd.ins[1].bytes.data(), host_out.data(), &pass_ms)) {
+      if (int rc = one_pass(host_out, &pass_ms)) {
         g_err = sg.err;
         return finish(rc);
       }
@@ -1622,6 +1781,46 @@ int uk_stream_gemm(const char* hcs_json, const uk_op_desc* d, const uk_plan* pla
   return UK_OK;
 }
 
+int uk_stream_gemm_file(const char* hcs_json, const uk_op_desc* d, const uk_plan* plan, const char* a_path,
+                        const void* hB, void* hC, double* pass_ms) {
+  if (!a_path || !hB || !hC)
+    return fail(UK_BAD_INVOCATION, "UNIKERN_ERROR what=bad_invocation reason=null file path or host operand");
+  Hcs h;
+  std::string e;
+  if (!load_hcs(hcs_json, &h, &e)) return fail(UK_BAD_INVOCATION, "UNIKERN_ERROR what=hcs reason=" + e);
+  KmlTree t;
+  Plan p;
+  if (int rc = prepare(d, plan, &h, &t, &p)) return rc;
+  if (!(t.op == OpKind::Gemm && (t.dtype == DType::F16 || t.dtype == DType::F32)))
+    return fail(UK_BAD_INVOCATION, "UNIKERN_ERROR what=bad_invocation reason=only an f16 or f32 GEMM streams");
+  const Shape s = shape_of(t);
+  const int64_t need = s.M * s.K * (t.dtype == DType::F16 ? 2 : 4);
+  struct Fd {
+    int fd = -1;
+    ~Fd() {
+      if (fd >= 0) ::close(fd);
+    }
+  } f;
+  f.fd = ::open(a_path, O_RDONLY | O_CLOEXEC);
+  if (f.fd < 0)
+    return fail(UK_BAD_INVOCATION, std::string("UNIKERN_ERROR what=mmap_open path=") + a_path + " msg=" +
+                                       std::strerror(errno));
+  struct stat sb;
+  if (::fstat(f.fd, &sb) != 0 || int64_t(sb.st_size) < need)
+    return fail(UK_BAD_INVOCATION, "UNIKERN_ERROR what=mmap_short_file need=" + std::to_string(need) +
+                                       " have=" + std::to_string(int64_t(sb.st_size)));
+  if (device_ok(nullptr) != UK_OK) return fail(UK_HIP_FAILURE, "UNIKERN_ERROR what=device reason=not gfx950");
+  if (p.shard_rows <= 0) p.shard_rows = int(std::min<int64_t>(s.M, INT32_MAX));
+  p.stream_path = 2;
+  DevArena arena;
+  StreamGemm sg;
+  if (int rc = sg.setup(t, p, arena, 2)) return fail(rc, sg.err);
+  double ms = 0;
+  if (int rc = sg.pass_file(f.fd, hB, hC, &ms)) return fail(rc, sg.err);
+  if (pass_ms) *pass_ms = ms;
+  return UK_OK;
+}
+
 int uk_fill_uniform(float* o, size_t n, uint64_t seed, float lo, float hi) {
   if (!o && n) return UK_BAD_INVOCATION;
   fill_uniform(o, n, seed, lo, hi);
@@ -1734,6 +1933,10 @@ int uk_ledger_lookup(void* ledger, const char* hcs_json, const char* kml_json, u
     plan->predicted_us = row->c_ms * 1e3;
     plan->feasible = 1;
     plan->shard_rows = shard;
+    // The mapped scenario-B path is recorded in the plan key (the solver's "+stream_mmap").
+    const std::string mm = "+stream_mmap";
+    const bool mapped = key.size() >= mm.size() && key.compare(key.size() - mm.size(), mm.size(), mm) == 0;
+    plan->stream_path = shard > 0 ? (mapped ? 2 : 1) : 0;
     std::snprintf(plan->key, sizeof plan->key, "%s", key.c_str());
   }
   if (c_ms) *c_ms = row->c_ms;

@@ -554,14 +554,60 @@ std::optional<Plan> solve_stream_gemm(const Hcs& h, const KmlTree& t, const Shap
   Plan p = *kp;
   const int64_t shards = (s.M + rows - 1) / rows;
   const double link_gbps = h.link_bw_gbps > 0 ? h.link_bw_gbps : 1.0;
-  const double copy_us = double(workload_of(t).bytes) / (link_gbps * 1e3);
+  const double bytes = double(workload_of(t).bytes);
+  const double overhead_us = double(shards) * launch_us(h);
   p.shard_rows = int(rows);
-  p.predicted_us = std::max(kp->predicted_us, copy_us) + double(shards) * launch_us(h);
-  p.key = kp->key + "+stream";
-  p.why = "scenario B: " + std::to_string(shards) + " M-shards of " + std::to_string(rows) + " rows through pinned " +
-          "host buffers, B resident (" + std::to_string(b_bytes) + " B), link " + fmt("%.0f", link_gbps) +
-          " GB/s; kernel " + kp->key;
-  return p;
+  // Two data paths for A (reference src/solver.cpp:14-44, :96-121). Pinned copies move every byte
+  // over the link once and overlap the kernels. The mapped path pages A in from storage (the
+  // nvme tier) and the kernel reads it over the link once per workgroup column that consumes
+  // it (ceil(N / tile_n)); B and C move as copies. Its copy term is the pinned one plus two
+  // non-negative terms, so the pinned path wins by the cost model; the mapped candidate exists
+  // only where the description has an nvme tier (a named predicate otherwise).
+  std::vector<Cand> cs;
+  {
+    Cand c;
+    c.plan = p;
+    c.plan.stream_path = 1;
+    c.plan.key = kp->key + "+stream";
+    c.cost = std::max(kp->predicted_us, bytes / (link_gbps * 1e3)) + overhead_us;
+    c.plan.why = "scenario B: " + std::to_string(shards) + " M-shards of " + std::to_string(rows) +
+                 " rows through pinned host buffers, B resident (" + std::to_string(b_bytes) + " B), link " +
+                 fmt("%.0f", link_gbps) + " GB/s; kernel " + kp->key;
+    cs.push_back(c);
+  }
+  const double nvme_gbps = h.tier_bw("nvme");
+  if (nvme_gbps <= 0) {
+    reject(log, kp->key + "+stream_mmap violates mmap_stream_requires_nvme_tier_bw>0");
+  } else {
+    const double streamed = double(s.M * s.K * es);
+    const int64_t reuse = (s.N + std::max(1, kp->tile_n) - 1) / std::max(1, kp->tile_n);
+    const double copy_us = streamed / (nvme_gbps * 1e3) + streamed * double(reuse) / (link_gbps * 1e3) +
+                           (bytes - streamed) / (link_gbps * 1e3);
+    Cand c;
+    c.plan = p;
+    c.plan.stream_path = 2;
+    c.plan.key = kp->key + "+stream_mmap";
+    c.cost = std::max(kp->predicted_us, copy_us) + overhead_us;
+    c.plan.why = "scenario B: " + std::to_string(shards) + " M-shards of " + std::to_string(rows) +
+                 " rows, A read by the kernel from host-mapped staging (read " + std::to_string(reuse) +
+                 " times over the link), B resident, nvme " + fmt("%.0f", nvme_gbps) + " GB/s, link " +
+                 fmt("%.0f", link_gbps) + " GB/s; kernel " + kp->key;
+    cs.push_back(c);
+  }
+  const Cand* best = &cs[0];
+  for (const Cand& c : cs)
+    if (c.cost < best->cost || (c.cost == best->cost && c.plan.key < best->plan.key)) best = &c;
+  if (log) {
+    for (const Cand& c : cs)
+      log->ranked.emplace_back(c.cost, c.plan.key + " family=" + std::to_string(int(c.plan.family)) +
+                                           " variant=" + std::to_string(c.plan.variant) +
+                                           " stream_path=" + (c.plan.stream_path == 2 ? "mmap" : "pinned"));
+    std::sort(log->ranked.begin(), log->ranked.end());
+  }
+  Plan out = best->plan;
+  out.predicted_us = best->cost;
+  out.feasible = kp->feasible * int(cs.size());  // every kernel candidate with each data path
+  return out;
 }
 
 }  // namespace

@@ -161,6 +161,8 @@ struct Plan {
   int feasible = 0;     // |X|, candidates that passed the predicates
   int shard_rows = 0;   // > 0: scenario B, the GEMM streams A and C through pinned host memory in
                         // M-shards of this many rows with B resident (0: everything resident)
+  int stream_path = 0;  // scenario B's path for A: 1 pinned copies, 2 host-mapped staging read by
+                        // the kernel (0 when resident)
   std::string key;      // canonical candidate key (tie-break)
   std::string why;      // one-line account of the choice
 };
