@@ -252,6 +252,22 @@ def test_cli_violation_resolve_commit(uk, tmp_path, ledger):
         assert L.lookup(kml) is None and L.lookup(kml, tight) is not None
 
 
+def test_cli_pinned_arm_is_not_committed(uk, tmp_path):
+    # A run whose executed data path is not the plan's (UK_GEMM_STREAM_PATH pinned an experiment
+    # arm) verifies but lands in no ledger row (reference src/main.cpp:544-556): the plan here
+    # takes the pinned path, the recorded run says it ran the mapped one.
+    arm = OK_LINE.replace("mode=resident", "mode=streamed stream_path=mmap")
+    rc, out, err = _run(uk, tmp_path, _outcomes(tmp_path, (0, arm)))
+    assert rc == 0, out + err
+    assert "LEDGER SKIP reason=env_path_pin executed=mmap planned=pinned" in out and "LEDGER COMMIT" not in out
+    with uk.Ledger(tmp_path / "l.jsonl") as L:
+        assert L.size() == (0, 0)
+    # The plan's own path commits.
+    same = OK_LINE.replace("mode=resident", "mode=streamed stream_path=pinned")
+    rc, out, err = _run(uk, tmp_path, _outcomes(tmp_path, (0, same)))
+    assert rc == 0 and "LEDGER COMMIT" in out and "LEDGER SKIP" not in out, out + err
+
+
 def test_cli_refusal_without_denominator(uk, tmp_path):
     # The guard's own refusal (exit 5, no result line): rate 1.0, re-solve, retry clean.
     refusal = ("UNIKERN_ERROR what=oversubscription ptr=in type=3 migrations=1 checks=0 vram_free=8407547904 "

@@ -465,6 +465,17 @@ int cmd_run(int argc, char** argv, bool write_ledger) {
     uk_ledger_close(ledger);
     return x.rc == UK_OK ? 1 : x.rc;
   }
+  // A run whose executed data path differs from the plan's (UK_GEMM_STREAM_PATH pinned an
+  // experiment arm) verifies but is not committed: its time is another path's, and under the
+  // plan's key it would enter calibration as the plan's (reference src/main.cpp:544-556).
+  const std::string planned = plan.stream_path == 2 ? "mmap" : "pinned";
+  const std::string executed(x.r.stream_path, strnlen(x.r.stream_path, sizeof x.r.stream_path));
+  if (!executed.empty() && executed != planned) {
+    std::cout << "LEDGER SKIP reason=env_path_pin executed=" << executed << " planned=" << planned
+              << " (verify=PASS; the plan's row keeps its own path's measurement)\n";
+    uk_ledger_close(ledger);
+    return 0;
+  }
   if (!write_ledger) {
     std::cout << "VERIFY PASS (no ledger write)\n";
     uk_ledger_close(ledger);
