@@ -167,6 +167,26 @@ def test_softmax_huge_maxima(gpu, vi):
     check_rows_op(Y, O.softmax(X), softmax64(X), C)
 
 
+@pytest.mark.parametrize("vi", [None, 11, 17, 24])
+def test_softmax_non_finite_rows(gpu, vi):
+    # The reference's loop (src/codegen_hip.cpp:1999-2009) on non-finite inputs: a -inf element
+    # under a finite maximum gives exactly 0, a row holding +inf or only -inf gives NaN
+    # throughout (inf - inf), and a row with one finite element gives exactly 1 there.
+    L, C = 6, 4096
+    X = O.normal(L * C, 91, 0.0, 8.0).reshape(L, C).copy()
+    X[1, ::7] = -np.inf
+    X[2, 100] = np.inf
+    X[3, :] = -np.inf
+    X[4, :] = -np.inf
+    X[4, 4095] = 3.0
+    Y = run_op(gpu, "softmax", X, plan=None if vi is None else rows_plan(gpu, vi))
+    R = O.softmax(X)
+    assert np.array_equal(np.isnan(Y), np.isnan(R)) and np.isnan(Y[2]).all() and np.isnan(Y[3]).all()
+    assert np.all(Y[1, ::7] == 0.0) and Y[4, 4095] == 1.0 and np.all(Y[4, :4095] == 0.0)
+    ok = ~np.isnan(R)
+    assert np.all(np.abs(Y[ok] - R[ok]) <= 1e-5 * np.maximum(np.abs(R[ok]), 1e-6))
+
+
 @pytest.mark.parametrize("L,C", [(4096, 4096), (65536, 256), (3, 7), (1, 1), (5, 12), (37, 4096), (6, 2052),
                                  (5, 3000), (2, 2048), (3, 4100)])
 def test_channelscale_bit_exact(gpu, L, C):
