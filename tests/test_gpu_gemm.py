@@ -18,7 +18,8 @@ pytestmark = pytest.mark.gpu
 # v_mfma_f32_16x16x32_f16.
 F16_VARIANTS = [(256, 256, 32), (256, 256, 32), (256, 256, 32), (256, 256, 32), (256, 128, 32), (256, 128, 64),
                 (128, 128, 64), (128, 128, 32), (256, 256, 32), (256, 256, 32), (256, 256, 32), (256, 256, 32),
-                (256, 256, 32), (256, 256, 32), (256, 256, 32), (256, 256, 32), (256, 256, 32), (256, 256, 64), (256, 256, 64)]
+                (256, 256, 32), (256, 256, 32), (256, 256, 32), (256, 256, 32), (256, 256, 32), (256, 256, 64), (256, 256, 64),
+                (256, 256, 64)]
 
 
 def gemm_gpu(uk, A, B, dtype, layout, plan=None):

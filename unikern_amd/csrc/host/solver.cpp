@@ -209,7 +209,13 @@ std::optional<Plan> solve_gemm(const Hcs& h, const KmlTree& t, const Shape& s, S
       const GemmF16Variant v = kGemmF16Variants[i];
       std::ostringstream key;
       key << "gemm_f16:" << v.bm << "x" << v.bn << "x" << v.bk << ",w" << v.wm << "x" << v.wn << ",s" << v.stages << ",z" << v.swz
-          << (v.pp == 1 ? ",pp" : v.pp == 2 ? ",w4" : v.pp == 3 ? ",w4s" : v.pp == 4 ? ",w4k" : v.pp == 5 ? ",w4k16" : "");
+          << (v.pp == 1   ? ",pp"
+              : v.pp == 2 ? ",w4"
+              : v.pp == 3 ? ",w4s"
+              : v.pp == 4 ? ",w4k"
+              : v.pp == 5 ? ",w4k16"
+              : v.pp == 6 ? ",w8k16"
+                          : "");
       if (s.M % v.bm || s.N % v.bn || s.K % v.bk) {
         reject(log, key.str() + " violates M%bm==0 && N%bn==0 && K%bk==0");
         continue;
@@ -217,7 +223,7 @@ std::optional<Plan> solve_gemm(const Hcs& h, const KmlTree& t, const Shape& s, S
       const int waves = v.wm * v.wn;
       const int64_t stage_bytes = int64_t(v.bm + v.bn) * v.bk * 2;
       const int64_t epi_bytes = int64_t(waves) * (v.bm / v.wm) * ((v.bn / v.wn) * 2 + 16);
-      // The 64-deep four-wavefront kernels (pp = 4, 5) keep five operand slots: two for A, three for B.
+      // The 64-deep kernels (pp = 4, 5, 6) keep five operand slots: two for A, three for B.
       const int64_t ring = v.pp >= 4 ? 5 * int64_t(v.bm) * v.bk * 2 : v.stages * stage_bytes;
       const int64_t lds = std::max<int64_t>(ring, epi_bytes);
       if (lds > lds_block(h)) {

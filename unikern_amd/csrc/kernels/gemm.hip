@@ -1159,6 +1159,165 @@ __global__ void __launch_bounds__(256, 1)
 }
 
 // ---------------------------------------------------------------------------------------
+// gemm_f16_w8k16_kernel: the 256x256x64 tile, slots and copy schedule of gemm_f16_w4k16_kernel
+// with eight wavefronts, two per SIMD, each a 128x64 wave tile (8 x 4 accumulator tuples, 128
+// AGPRs, so that two wavefronts share a SIMD's registers); per 64-deep tile each wavefront issues
+// two k-steps of 32 MFMAs, 12 fragment reads for the next k-step and four copies. Kept beside the
+// pick as the measured answer to whether a second wavefront per SIMD, multiplying while the other
+// reads and copies, hides the data movement: it reads 1.5 times the LDS bytes per flop, and at
+// 4096^3 it ran 104.3-106.0 us against 97.1-98.9 us for gemm_f16_w4k16_kernel (same bits, one box).
+// ---------------------------------------------------------------------------------------
+constexpr int kW8WM = 128, kW8WN = 64;
+constexpr int kW8Pitch = kW8WN * 2 + 16;
+static_assert(8 * kW8WM * kW8Pitch <= kW4kLds, "epilogue staging fits");
+
+__global__ void __launch_bounds__(512, 1)
+    gemm_f16_w8k16_kernel(const _Float16* __restrict__ A, const _Float16* __restrict__ B, _Float16* __restrict__ C,
+                          int M, int N, int K, int tiles_m, int tiles_n) {
+  asm volatile("" ::"s"(A), "s"(B), "s"(C), "s"(M), "s"(N), "s"(K), "s"(tiles_m), "s"(tiles_n));
+  typedef float f32x4v __attribute__((ext_vector_type(4)));
+  __shared__ __attribute__((aligned(1024))) char lds[kW4kLds];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = w >> 2, wn = w & 3;
+
+  const int G = gridDim.x;
+  int lin = blockIdx.x;
+  if ((G & 7) == 0) lin = (lin & 7) * (G >> 3) + (lin >> 3);
+  constexpr int kGroupM = 4;
+  const int per_group = kGroupM * tiles_n;
+  const int group = lin / per_group;
+  const int first_m = group * kGroupM;
+  const int gm = (tiles_m - first_m) < kGroupM ? (tiles_m - first_m) : kGroupM;
+  const int in_group = lin - group * per_group;
+  const int tm = first_m + in_group % gm;
+  const int tn = in_group / gm;
+  const int m0 = tm * kW4BM, n0 = tn * kW4BN;
+
+  const _Float16* Ab = A + (int64_t)m0 * K;
+  const _Float16* Bb = B + (int64_t)n0 * K;
+  const int panel = 256 * K * 2;
+  const int lrow = (lane >> 3) * K * 2;
+  const int ve = lrow + (((lane & 7) ^ (lane >> 4)) << 4);
+  const int vo = lrow + (((lane & 7) ^ (lane >> 4) ^ 4) << 4);
+  const int step = 8 * K * 2;
+  const int KT = K / kW4kBK;
+  // Copy u (< 4) of this wavefront's 32 rows of an operand tile: rows w 32 + 8 u .. + 8.
+  auto copy_q = [&](auto q_c, const void* base, char* dst, int t) {
+    constexpr int u = decltype(q_c)::value;
+    const bool live = t < KT;
+    const int voff = live ? ((u & 1) ? vo : ve) : kCopyNone;
+    const int soff = ((w * 32) * K + (live ? t : 0) * kW4kBK) * 2;
+    copy_u_to_lds<u>(base, panel, dst + w * 4 * 1024, voff, soff, step);
+  };
+
+  const int frow = lane & 15, fk = lane >> 4;
+  const int fsw = (frow >> 1) & 7;
+  const int a_row = (wm * kW8WM + frow) * kW4kRow, b_row = (wn * kW8WN + frow) * kW4kRow;
+  f16x8 fa[2][8], fb[2][4];
+  f32x4v acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4v{0.f, 0.f, 0.f, 0.f};
+
+  // Read r < 12 in the order the MFMAs consume them: A0, B0..B3, A1..A7.
+  auto read = [&](auto buf_c, auto r_c, const char* ab, const char* bb) {
+    constexpr int buf = decltype(buf_c)::value, r = decltype(r_c)::value;
+    if constexpr (r == 0) fa[buf][0] = *reinterpret_cast<const f16x8*>(ab);
+    else if constexpr (r <= 4) fb[buf][r - 1] = *reinterpret_cast<const f16x8*>(bb + (r - 1) * 16 * kW4kRow);
+    else fa[buf][r - 4] = *reinterpret_cast<const f16x8*>(ab + (r - 4) * 16 * kW4kRow);
+  };
+  // MFMA m (< 32) on set CUR, serpentine over the 8 x 4 tuples; read r of the next set after MFMA
+  // (8 r) / 3; copy q after MFMA 8 q + 3.
+  auto mstep = [&](auto cur_c, auto m_c, auto op_c, const char* ab, const char* bb, char* cdst, int tc) {
+    constexpr int cur = decltype(cur_c)::value, m = decltype(m_c)::value;
+    constexpr int i = m >> 2, j = (i & 1) ? 3 - (m & 3) : (m & 3);
+    __asm__ volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(acc[i][j]) : "v"(fb[cur][j]), "v"(fa[cur][i]));
+    [&]<int... Rs>(std::integer_sequence<int, Rs...>) {
+      ((((8 * Rs) / 3 == m) ? (read(std::integral_constant<int, cur ^ 1>{}, std::integral_constant<int, Rs>{}, ab, bb), 0)
+                            : 0),
+       ...);
+    }(std::make_integer_sequence<int, 12>{});
+    if constexpr (m % 8 == 3)
+      copy_q(std::integral_constant<int, m / 8>{},
+             decltype(op_c)::value == 0 ? static_cast<const void*>(Ab) : static_cast<const void*>(Bb), cdst, tc);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto kstep = [&](auto cur_c, auto op_c, const char* ab, const char* bb, char* cdst, int tc) {
+    [&]<int... Ms>(std::integer_sequence<int, Ms...>) {
+      (mstep(cur_c, std::integral_constant<int, Ms>{}, op_c, ab, bb, cdst, tc), ...);
+    }(std::make_integer_sequence<int, 32>{});
+  };
+  auto frag_ptrs = [&](int as, int bs, int ks, const char** ab, const char** bb) {
+    const int c = ((4 * ks + fk) ^ fsw) << 4;
+    *ab = lds + as * kW4kOp + a_row + c;
+    *bb = lds + kW4kB0 + bs * kW4kOp + b_row + c;
+  };
+  auto read_all = [&](auto buf_c, const char* ab, const char* bb) {
+    [&]<int... Rs>(std::integer_sequence<int, Rs...>) { (read(buf_c, std::integral_constant<int, Rs>{}, ab, bb), ...); }(
+        std::make_integer_sequence<int, 12>{});
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+
+  [&]<int... Qs>(std::integer_sequence<int, Qs...>) {
+    (copy_q(std::integral_constant<int, Qs>{}, Bb, lds + kW4kB0, 0), ...);
+    (copy_q(std::integral_constant<int, Qs>{}, Ab, lds, 0), ...);
+    (copy_q(std::integral_constant<int, Qs>{}, Bb, lds + kW4kB0 + kW4kOp, 1), ...);
+    (copy_q(std::integral_constant<int, Qs>{}, Ab, lds + kW4kOp, 1), ...);
+  }(std::make_integer_sequence<int, 4>{});
+  wait_vmcnt<8>();
+  barrier_nofence();
+  {
+    const char *ab, *bb;
+    frag_ptrs(0, 0, 0, &ab, &bb);
+    read_all(I0{}, ab, bb);
+  }
+  int as = 0, bs = 0;
+  for (int t = 0; t < KT; ++t) {
+    const int as1 = as ^ 1, bs1 = bs == 2 ? 0 : bs + 1, bs2 = bs == 0 ? 2 : bs - 1;
+    const char *ab, *bb;
+    frag_ptrs(as, bs, 1, &ab, &bb);  // k-step 1's fragments, read during k-step 0
+    kstep(I0{}, I1{}, ab, bb, lds + kW4kB0 + bs2 * kW4kOp, t + 2);
+    wait_vmcnt<4>();
+    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    barrier_nofence();
+    frag_ptrs(as1, bs1, 0, &ab, &bb);  // tile t + 1's first fragments
+    kstep(I1{}, I0{}, ab, bb, lds + as * kW4kOp, t + 2);
+    as = as1;
+    bs = bs1;
+  }
+  __asm__ volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  wait_vmcnt<0>();
+  __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  barrier_nofence();
+  char* stage = lds + w * (kW8WM * kW8Pitch);
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      f16x4 h;
+      h[0] = (_Float16)acc[i][j][0];
+      h[1] = (_Float16)acc[i][j][1];
+      h[2] = (_Float16)acc[i][j][2];
+      h[3] = (_Float16)acc[i][j][3];
+      const int m = i * 16 + (lane & 15);
+      const int n = j * 16 + 4 * (lane >> 4);
+      *reinterpret_cast<f16x4*>(stage + m * kW8Pitch + n * 2) = h;
+    }
+  __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  constexpr int kRowChunks = kW8WN * 2 / 16;
+  _Float16* Cw = C + (int64_t)(m0 + wm * kW8WM) * N + n0 + wn * kW8WN;
+#pragma unroll 4
+  for (int id = lane; id < kW8WM * kRowChunks; id += 64) {
+    const int r = id / kRowChunks, c = id % kRowChunks;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(stage + r * kW8Pitch + c * 16);
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(Cw + (int64_t)r * N + c * 8));
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // f32 GEMM, 64x64x64 tiles, eight wavefronts (two k halves x 2x2 quarters).
 // ---------------------------------------------------------------------------------------
 constexpr int kF32Pitch = 68;  // floats per staged row (64 + 4 padding)
@@ -1331,7 +1490,15 @@ namespace {
 template <int I>
 hipError_t gemm_f16_variant(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, hipStream_t s) {
   constexpr GemmF16Variant v = kGemmF16Variants[I];
-  if constexpr (v.pp == 4 || v.pp == 5) {
+  if constexpr (v.pp == 6) {
+    static_assert(v.bm == kern::kW4BM && v.bn == kern::kW4BN && v.bk == kern::kW4kBK && v.wm == 2 && v.wn == 4,
+                  "the eight-wavefront variant is 256x256x64 with 2x4 wavefronts");
+    const int tiles_m = int(M / v.bm), tiles_n = int(N / v.bn);
+    hipLaunchKernelGGL(kern::gemm_f16_w8k16_kernel, dim3((unsigned)(tiles_m * tiles_n)), dim3(512), 0, s,
+                       static_cast<const _Float16*>(A), static_cast<const _Float16*>(B), static_cast<_Float16*>(C),
+                       (int)M, (int)N, (int)K, tiles_m, tiles_n);
+    return hipGetLastError();
+  } else if constexpr (v.pp == 4 || v.pp == 5) {
     static_assert(v.bm == kern::kW4BM && v.bn == kern::kW4BN && v.bk == kern::kW4kBK && v.wm * v.wn == 4 &&
                       v.stages == 2,
                   "the 64-deep four-wavefront variants are 256x256x64 with two A slots");
@@ -1386,7 +1553,7 @@ hipError_t launch_gemm_f16(const Plan& p, const void* A, const void* B, void* C,
   if (int64_t(v.bm > v.bn ? v.bm : v.bn) * K * 2 > INT32_MAX) return hipErrorInvalidValue;
   if ((((uintptr_t)A) | ((uintptr_t)B) | ((uintptr_t)C)) & 15) return hipErrorInvalidValue;
   if ((M / v.bm) * (N / v.bn) > INT32_MAX) return hipErrorInvalidValue;
-  static_assert(kNumGemmF16Variants == 19, "every GEMM variant needs a case below");
+  static_assert(kNumGemmF16Variants == 20, "every GEMM variant needs a case below");
   switch (p.variant) {
 #define UK_GEMM_CASE(I) \
   case I:                 \
@@ -1410,6 +1577,7 @@ hipError_t launch_gemm_f16(const Plan& p, const void* A, const void* B, void* C,
     UK_GEMM_CASE(16)
     UK_GEMM_CASE(17)
     UK_GEMM_CASE(18)
+    UK_GEMM_CASE(19)
 #undef UK_GEMM_CASE
     default: return hipErrorInvalidValue;
   }

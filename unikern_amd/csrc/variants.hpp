@@ -69,7 +69,8 @@ constexpr int kReduceThreads = 256;
 // wavefronts on v_mfma_f32_16x16x32_f16 with a rolling A fragment (gemm_f16_w4s_kernel); pp = 4:
 // the pp = 2 tiling with 64-deep k-tiles in 128-byte rows, two A and three B tile slots
 // (gemm_f16_w4k_kernel; stages counts the A slots); pp = 5: the same on v_mfma_f32_16x16x32_f16
-// (gemm_f16_w4k16_kernel). eff is
+// (gemm_f16_w4k16_kernel); pp = 6: that tile with eight wavefronts of 128x64, two per SIMD
+// (gemm_f16_w8k16_kernel). eff is
 // the calibrated fraction of the dense f16 MFMA peak the variant sustains when every CU holds a
 // tile (kernel-only median at M = N = K = 4096 on one MI355X, clocks settled); the solver's cost
 // model scales it by wave quantisation for other shapes.
@@ -98,6 +99,7 @@ constexpr GemmF16Variant kGemmF16Variants[] = {
     {256, 256, 32, 2, 2, 4, 1, 0.440, 3},
     {256, 256, 64, 2, 2, 2, 1, 0.487, 4},
     {256, 256, 64, 2, 2, 2, 1, 0.545, 5},
+    {256, 256, 64, 2, 4, 2, 1, 0.517, 6},
 };
 constexpr int kNumGemmF16Variants = sizeof(kGemmF16Variants) / sizeof(kGemmF16Variants[0]);
 
