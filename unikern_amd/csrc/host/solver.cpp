@@ -336,6 +336,47 @@ std::optional<Plan> solve_q8(const Hcs& h, const KmlTree& t, const Shape& s, Sol
   const int64_t npairs = s.K / 64;
   for (int i = 0; i < kNumQ8Variants; ++i) {
     const Q8Variant v = kQ8Variants[i];
+    if (v.gemv) {
+      // One weight row per wavefront (M = 1): the weight stream in whole rows, the activation row
+      // read from L2 once per workgroup, and the last row's vector-ALU reduction after it lands.
+      const std::string key = "q8_0:gemv,waves=" + std::to_string(v.waves) + ",pl=" + std::to_string(v.pairs);
+      const int64_t lds = int64_t(v.waves) * 17 * 64 * v.pairs * 4 + 64 * v.pairs * 128;
+      if (s.M != 1) {
+        reject(log, key + " violates M==1");
+        continue;
+      }
+      if (s.K % 256 != 0 || npairs > 64 * v.pairs) {
+        reject(log, key + " violates K%256==0 && K<=" + std::to_string(4096 * v.pairs));
+        continue;
+      }
+      if (lds > lds_block(h)) {
+        reject(log, key + " violates LDS " + std::to_string(lds) + " <= " + std::to_string(lds_block(h)));
+        continue;
+      }
+      const int64_t grid = (s.N + v.waves - 1) / v.waves;
+      const int resident =
+          std::max(1, std::min<int>(waves_by_regs(h, 64) * simds(h) / v.waves, int(lds_cu(h) / lds)));
+      const double inflight = double(v.waves) * double(npairs) * 68.0;
+      const double stream = stream_us(h, double(w.bytes), grid, resident, inflight, false, 0.0, kQ8LatencyUs);
+      const double act_cu = std::ceil(double(grid) / cus(h)) * double(s.K) * 2.0;
+      // The last wavefront's reduction (about 170 vector instructions per lane per 64 pairs, a
+      // quarter of a latency at K = 4096) runs after its row lands.
+      const double tail_us = 0.25 * kQ8LatencyUs * double(v.pairs);
+      Cand c;
+      c.plan.family = Family::Q8Gemm;
+      c.plan.variant = i;
+      c.plan.threads = v.waves * 64;
+      c.plan.split_k = 1;
+      c.plan.tile_k = int(s.K);
+      c.plan.grid = grid;
+      c.plan.key = key;
+      c.plan.why = std::to_string(grid) + " workgroups of " + std::to_string(v.waves) +
+                   " weight rows (one per wavefront), vector-ALU dot products, " + std::to_string(resident) +
+                   " resident per CU";
+      c.cost = launch_us(h) + stream + act_cu / kActBytesPerUsPerCu + tail_us;
+      cs.push_back(c);
+      continue;
+    }
     std::ostringstream key;
     key << "q8_0:waves=" << v.waves << ",pairs=" << v.pairs << ",vec=" << v.vec << (v.db ? ",db" : "");
     if (v.nt > 1) key << ",nt=" << v.nt;

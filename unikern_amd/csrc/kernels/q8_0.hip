@@ -322,11 +322,161 @@ __global__ void __launch_bounds__(WAVES * 64)
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// M = 1 (one activation row): q8_0_gemv_kernel. Without 16 activation rows the MFMA tile buys
+// nothing, so each wavefront owns one whole weight row and reduces it on the vector ALUs: the
+// row is K/32 * 34 contiguous bytes (4352 at K = 4096), copied into the wavefront's LDS area with
+// 1 KiB direct-to-LDS instructions (whole 128-byte lines except at the ends, where the tile
+// kernels copy 272-byte row segments), lane l takes block pairs l, l + 64, ... and a DPP
+// wavefront sum replaces the tile kernels' LDS fold and its barrier.
+// The activation row is copied into LDS once per workgroup (WAVES rows share it), 128 bytes per
+// block pair, with the eight 16-byte chunks of pair p rotated by p (slot s holds chunk
+// (s - p) mod 8): a lane reading chunk k of its pair reads slot (k + p) mod 8, so the 64 lanes'
+// 16-byte reads, 128 bytes apart, spread over the LDS banks instead of falling on two bank
+// groups (the unrotated layout measured 5.45 against 5.12 us at N = K = 4096).
+// Per block: 16 v_dot2_f32_f16 of the quants (as binary16, exact, by the 1024-bias trick of
+// q4_to_f16) with the activations, f32 accumulation; the pair adds d_odd * s_odd + d_even * s_even
+// and a lane's pairs add in order; the wavefront sum is a fixed DPP tree (deterministic).
+// K: a multiple of 256 (16-byte aligned rows of whole block-pair quadruples), at most 4096 PL.
+// Rows past N copy row N - 1 (valid memory) and are never stored. FULL: K = 4096 PL exactly, every
+// count a compile-time constant (the general form's run-time copy counts and wait cost 5.49 against
+// 5.12 us at N = K = 4096).
+// Four quants (one dword) -> binary16 -> s + q . x over four activations (two dwords).
+// The two f16 pairs enter __builtin_amdgcn_fdot2 as separate values: this compiler, given the
+// pairs packed into a two-dword vector (as q4_to_f16 returns them) and extracted again, fed the
+// low pair to both products (seen in its output for gfx950; the MFMA operands are not affected).
+__device__ __forceinline__ float q4_dot(uint32_t dw, uint32_t xa, uint32_t xb, float s) {
+  const uint32_t u = dw ^ 0x80808080u;
+  const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+  const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+  const f16x2v bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+  const f16x2v l = __builtin_bit_cast(f16x2v, lo) - bias, h = __builtin_bit_cast(f16x2v, hi) - bias;
+  s = __builtin_amdgcn_fdot2(l, __builtin_bit_cast(f16x2v, xa), s, false);
+  return __builtin_amdgcn_fdot2(h, __builtin_bit_cast(f16x2v, xb), s, false);
+}
+
+// s_waitcnt vmcnt(n) for a wave-uniform n known only at run time (n > 15: vmcnt(0), which waits
+// for more than asked and is still correct).
+__device__ __forceinline__ void q8_wait_vmcnt_rt(int n) {
+  switch (n) {
+    case 15: q8_wait_vmcnt<15>(); break;
+    case 14: q8_wait_vmcnt<14>(); break;
+    case 13: q8_wait_vmcnt<13>(); break;
+    case 12: q8_wait_vmcnt<12>(); break;
+    case 11: q8_wait_vmcnt<11>(); break;
+    case 10: q8_wait_vmcnt<10>(); break;
+    case 9: q8_wait_vmcnt<9>(); break;
+    case 8: q8_wait_vmcnt<8>(); break;
+    case 7: q8_wait_vmcnt<7>(); break;
+    case 6: q8_wait_vmcnt<6>(); break;
+    case 5: q8_wait_vmcnt<5>(); break;
+    case 4: q8_wait_vmcnt<4>(); break;
+    case 3: q8_wait_vmcnt<3>(); break;
+    case 2: q8_wait_vmcnt<2>(); break;
+    case 1: q8_wait_vmcnt<1>(); break;
+    default: q8_wait_vmcnt<0>(); break;
+  }
+}
+
+// Workgroup barrier without the memory fence of __syncthreads(), which would also wait for the
+// wavefront's weight copies; the activation copies are waited for explicitly before it.
+__device__ __forceinline__ void q8_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  __asm__ volatile("s_barrier" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int WAVES, int PL, bool FULL>
+__global__ void __launch_bounds__(WAVES * 64)
+    q8_0_gemv_kernel(const _Float16* __restrict__ X, const uint8_t* __restrict__ Wq, float* __restrict__ Y, int N,
+                     int K) {
+  asm volatile("" ::"s"(X), "s"(Wq), "s"(Y), "s"(N), "s"(K));
+  constexpr int kMaxPairs = 64 * PL;
+  constexpr int kRowDw = 17 * kMaxPairs;                        // the longest row, in dwords
+  constexpr int kInstMax = (kMaxPairs * 68 / 16 + 63) / 64;      // its 16-byte copy instructions
+  static_assert(kInstMax <= 15, "the weight copies fit the explicit vmcnt waits");
+  __shared__ __attribute__((aligned(16))) unsigned char xs[kMaxPairs * 128];
+  __shared__ __attribute__((aligned(16))) uint32_t wl[WAVES * kRowDw];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int npairs = FULL ? kMaxPairs : K >> 6;
+  const int units = npairs / 4 * 17;      // 16-byte units of a row (npairs is a multiple of 4)
+  const int ninst = (units + 63) >> 6;
+  const int n = blockIdx.x * WAVES + wave;
+  const int nn = n < N ? n : N - 1;
+
+  // Activation copies: instruction q covers pairs 8q .. 8q + 7, lanes 8j .. 8j + 7 pair 8q + j.
+  for (int q = wave; 8 * q < npairs; q += WAVES) {
+    const int pr = 8 * q + (lane >> 3);
+    const int ch = ((lane & 7) - pr) & 7;
+    if (pr < npairs)
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(X + pr * 64 + ch * 8),
+                                       (lds_void*)(xs + q * 1024), 16, 0, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  uint32_t* mine = wl + wave * kRowDw;
+  const uint8_t* row = Wq + (int64_t)nn * npairs * 68;
+#pragma unroll
+  for (int t = 0; t < kInstMax; ++t) {
+    if (t < ninst) {
+      const int u = t * 64 + lane;
+      if (u < units)
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(row + 16 * u),
+                                         (lds_void*)(mine + t * 256), 16, 0, 0);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  q8_wait_vmcnt_rt(ninst);  // this wavefront's activation copies have landed
+  q8_barrier();             // and every wavefront's
+  q8_wait_vmcnt<0>();
+
+  float y = 0.f;
+#pragma unroll
+  for (int j = 0; j < PL; ++j) {
+    const int p = lane + 64 * j;
+    if (p < npairs) {
+      const uint32_t* pw = mine + 17 * p;
+      uint32_t dw[17];
+#pragma unroll
+      for (int d = 0; d < 17; ++d) dw[d] = pw[d];
+      const unsigned char* xl = xs + 128 * p;
+      u32x4 xv[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) xv[k] = *reinterpret_cast<const u32x4*>(xl + 16 * ((k + p) & 7));
+      // Even block: quant dword k is bytes 2 + 4k .. 5 + 4k of the pair; odd block: dwords 9-16.
+      float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        s0 = q4_dot(__builtin_amdgcn_alignbyte(dw[k + 1], dw[k], 2), xv[k >> 1][(k & 1) * 2],
+                    xv[k >> 1][(k & 1) * 2 + 1], s0);
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        s1 = q4_dot(dw[9 + k], xv[4 + (k >> 1)][(k & 1) * 2], xv[4 + (k >> 1)][(k & 1) * 2 + 1], s1);
+      const float d0 = half_bits_to_float(dw[0]), d1 = half_bits_to_float(dw[8] >> 16);
+      y += fmaf(d1, s1, d0 * s0);
+    }
+  }
+  y = wave_sum(y);
+  if (lane == 0 && n < N) Y[n] = y;
+}
+
 }  // namespace uk::kern
 
 namespace uk {
 
 namespace {
+template <int WAVES, int PL>
+hipError_t q8_gemv_go(const void* X, const void* Wq, float* Y, int64_t N, int64_t K, hipStream_t s) {
+  const dim3 grid((unsigned)((N + WAVES - 1) / WAVES));
+  if (K == 4096 * PL)
+    hipLaunchKernelGGL((kern::q8_0_gemv_kernel<WAVES, PL, true>), grid, dim3(WAVES * 64), 0, s,
+                       static_cast<const _Float16*>(X), static_cast<const uint8_t*>(Wq), Y, (int)N, (int)K);
+  else
+    hipLaunchKernelGGL((kern::q8_0_gemv_kernel<WAVES, PL, false>), grid, dim3(WAVES * 64), 0, s,
+                       static_cast<const _Float16*>(X), static_cast<const uint8_t*>(Wq), Y, (int)N, (int)K);
+  return hipGetLastError();
+}
+
 // LDS bytes of an instantiation: the weight staging plus the activation slices of XL rows.
 constexpr int q8_lds_bytes(int waves, int p, int vec, bool db, int nt, int xl) {
   return waves * nt * 16 * 17 * p * 4 * (db ? 2 : 1) + (xl ? waves * xl * 64 * p * 2 : 16);
@@ -386,6 +536,14 @@ hipError_t launch_q8_gemm(const Plan& p, const void* X, const void* Wq, float* Y
   // aligned when X is); the weight stream is copied as dwords (4-byte aligned rows and pairs).
   if ((((uintptr_t)X) & 15) || (((uintptr_t)Wq) & 3) || (((uintptr_t)Y) & 3)) return hipErrorInvalidValue;
   const Q8Variant v = kQ8Variants[p.variant];
+  if (v.gemv) {
+    // One activation row; rows of whole block-pair quadruples (16-byte aligned), at most 64 pairs
+    // per lane set.
+    if (M != 1 || K % 256 != 0 || K > 4096 * v.pairs || (((uintptr_t)Wq) & 15)) return hipErrorInvalidValue;
+    if (v.waves == 4 && v.pairs == 1) return q8_gemv_go<4, 1>(X, Wq, Y, N, K, s);
+    if (v.waves == 4 && v.pairs == 2) return q8_gemv_go<4, 2>(X, Wq, Y, N, K, s);
+    return hipErrorInvalidValue;
+  }
   // 16-byte copies: every wavefront segment (64 P elements of K) starts 16-byte aligned.
   if (v.vec == 4 && ((K % (64 * v.pairs)) != 0 || (((uintptr_t)Wq) & 15))) return hipErrorInvalidValue;
 #define UK_Q8_CASE(W, PV, VV, DBV, NTV)                                                          \
