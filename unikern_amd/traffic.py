@@ -32,7 +32,7 @@ KERNELS = {
     "gemm_f32": re.compile(r"gemm_f32_kernel"),
     "gemm_generic": re.compile(r"gemm_generic_kernel"),
     "conv": re.compile(r"conv_igemm_kernel|conv_tile_kernel|conv_lds_kernel|conv_lds16_kernel"),
-    "q8_0": re.compile(r"q8_0_gemm_kernel"),
+    "q8_0": re.compile(r"q8_0_gemm_kernel|q8_0_gemv_kernel"),
 }
 COPY_BYTES_READ = 4096 * 4096 * 4 + 4096 * 4
 COPY_BYTES_WRITTEN = 4096 * 4096 * 4
