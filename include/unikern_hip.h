@@ -169,6 +169,8 @@ int uk_solve(const char* hcs_json, const uk_op_desc* d, uk_plan* out, char* log,
  * uk_launch: enqueue the op on `stream` over caller-owned device buffers.
  *   gemm f32/f16:  in[0]=A, in[1]=B (layout NT: [K][N]; TN: [N][K]); out=C [M][N] (same dtype)
  *   gemm q8_0 TN:  in[0]=X f16 [M][K], in[1]=W blocks (N rows of K/32 blocks); out=Y f32 [M][N]
+ *                  (X 16-byte aligned, Y 4-byte; W 16-byte aligned where K is a multiple of 256,
+ *                  which every variant the solver picks there copies in 16-byte units, else 4-byte)
  *   conv NT:       in[0]=X [H][W][C], in[1]=Wt [Oc][Kh][Kw][C] (, in[2]=scale[Oc]); out=Y [Oc][Ho][Wo]
  *   conv NCHW:     in[0]=X [N][C][H][W], in[1]=W [Oc][C][Kh][Kw] (, in[2]=scale[Oc]); out=Y [N][Oc][Ho][Wo]
  *   reduce [L]:    in[0]=X; out=Y[1]           reduce [L,C]: in[0]=X; out=Y[L] (row sums)

@@ -84,3 +84,23 @@ def test_noalloc_gemm_f16_matches_launch(gpu):
         _launch(gpu, fn, d, ins, cb)
         outs.append(cb.download(np.uint16, (M, N)))
     assert np.array_equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_noalloc_q8_0_matches_launch(gpu, M):
+    # M = 1: the one-row-per-wavefront kernel; M = 16: the tile kernel. Neither needs scratch.
+    from test_gpu_q8_0 import make_weights
+
+    N, K = 1000, 4096
+    blocks, _, _ = make_weights(N, K, 908 + M)
+    Xh = O.f16_bits(O.normal(M * K, 909 + M, 0.0, 1.0)).reshape(M, K)
+    d = gpu.make_desc("gemm", [M, N, K], dtype="q8_0", layout="TN")
+    ins = [gpu.DeviceBuffer.from_array(Xh), gpu.DeviceBuffer.from_array(blocks)]
+    outs = []
+    for fn in (gpu.lib.uk_launch, gpu.lib.uk_launch_noalloc):
+        yb = gpu.DeviceBuffer(M * N * 4)
+        yb.fill(0xFF)
+        _launch(gpu, fn, d, ins, yb)
+        outs.append(yb.download(np.float32, (M, N)))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    assert np.linalg.norm(outs[0] - O.q8_0_gemm(Xh, blocks, N)) <= 1e-5 * np.linalg.norm(O.q8_0_gemm(Xh, blocks, N))
