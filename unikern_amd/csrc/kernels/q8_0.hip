@@ -25,7 +25,9 @@
 // lane's outputs all belong to one weight row and its two block scales are one LDS broadcast.
 //
 // K must be a multiple of 64 (whole block pairs per row).
-// Work split: grid.x = groups of 16 NT weight rows, grid.y = 16-row groups of activations. With
+// Two kernel forms: q8_0_gemm_kernel (MFMA tiles of 16 weight rows, any M) below, and
+// q8_0_gemv_kernel (M = 1: one weight row per wavefront on the vector ALUs) further down.
+// Work split of q8_0_gemm_kernel: grid.x = groups of 16 NT weight rows, grid.y = 16-row groups of activations. With
 // NT > 1 each activation fragment (read from global memory per workgroup) feeds NT MFMA tiles of
 // weights: every workgroup reads all of its activation rows over K, so for M = 16 the activation
 // reads (M K 2 bytes per workgroup, from L2) exceed the workgroup's weight bytes at NT = 1. A round
