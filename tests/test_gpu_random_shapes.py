@@ -70,6 +70,16 @@ def test_q8_0_random(gpu, M, N, kp):
     assert frob(q8_gpu(gpu, Xh, blocks, N), O.q8_0_gemm(Xh, blocks, N)) <= 1e-5
 
 
+@pytest.mark.parametrize("N,kq", draws(16, 10, (1, 3000), (1, 40)))
+def test_q8_0_decode_row_random(gpu, N, kq):
+    # One activation row, K a multiple of 256 up to 10240: the solver routes K <= 4096 to the
+    # one-row-per-wavefront kernel and longer K to the tile kernels.
+    K = 256 * kq
+    blocks, _, _ = make_weights(N, K, 7700 + N + kq)
+    Xh = O.f16_bits(O.normal(K, 7800 + N, 0.0, 1.0)).reshape(1, K)
+    assert frob(q8_gpu(gpu, Xh, blocks, N), O.q8_0_gemm(Xh, blocks, N)) <= 1e-5
+
+
 @pytest.mark.parametrize("L,C", draws(15, 8, (1, 300), (1, 6000)) + [(5, 4097), (9, 16384), (1, 1)])
 def test_rows_random(gpu, L, C):
     X = O.normal(L * C, 7600 + L, 0.0, 1.0).reshape(L, C)

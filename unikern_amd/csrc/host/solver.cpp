@@ -339,14 +339,14 @@ std::optional<Plan> solve_q8(const Hcs& h, const KmlTree& t, const Shape& s, Sol
     if (v.gemv) {
       // One weight row per wavefront (M = 1): the weight stream in whole rows, the activation row
       // read from L2 once per workgroup, and the last row's vector-ALU reduction after it lands.
-      const std::string key = "q8_0:gemv,waves=" + std::to_string(v.waves) + ",pl=" + std::to_string(v.pairs);
-      const int64_t lds = int64_t(v.waves) * 17 * 64 * v.pairs * 4 + 64 * v.pairs * 128;
+      const std::string key = "q8_0:gemv,waves=" + std::to_string(v.waves);
+      const int64_t lds = int64_t(v.waves) * 17 * 64 * 4 + 64 * 128;
       if (s.M != 1) {
         reject(log, key + " violates M==1");
         continue;
       }
-      if (s.K % 256 != 0 || npairs > 64 * v.pairs) {
-        reject(log, key + " violates K%256==0 && K<=" + std::to_string(4096 * v.pairs));
+      if (s.K % 256 != 0 || npairs > 64) {
+        reject(log, key + " violates K%256==0 && K<=4096");
         continue;
       }
       if (lds > lds_block(h)) {
@@ -361,7 +361,7 @@ std::optional<Plan> solve_q8(const Hcs& h, const KmlTree& t, const Shape& s, Sol
       const double act_cu = std::ceil(double(grid) / cus(h)) * double(s.K) * 2.0;
       // The last wavefront's reduction (about 170 vector instructions per lane per 64 pairs, a
       // quarter of a latency at K = 4096) runs after its row lands.
-      const double tail_us = 0.25 * kQ8LatencyUs * double(v.pairs);
+      const double tail_us = 0.25 * kQ8LatencyUs;
       Cand c;
       c.plan.family = Family::Q8Gemm;
       c.plan.variant = i;
@@ -391,7 +391,9 @@ std::optional<Plan> solve_q8(const Hcs& h, const KmlTree& t, const Shape& s, Sol
     }
     const int64_t per_round = int64_t(v.waves) * v.pairs;
     const int64_t rounds = (npairs + per_round - 1) / per_round;
-    // Pairs of the last round beyond K/64 are copied and skipped: wasted bandwidth.
+    // Pairs of the last round beyond K/64 re-copy pair 0 of the same rows and are skipped: those
+    // copies hit in L2 and cost issue, not HBM bytes (charged as HBM bytes, the 16-wavefront
+    // kernel was priced 1.4-1.7x its measured time at K = 4608-6144 and lost picks it wins).
     const double useful = double(npairs) / double(rounds * per_round);
     const int64_t grid = ((s.N + 16 * v.nt - 1) / (16 * v.nt)) * ((s.M + 15) / 16);
     // VGPRs per lane: activation fragments (8 per pair, twice with double buffering) and the
@@ -422,9 +424,9 @@ std::optional<Plan> solve_q8(const Hcs& h, const KmlTree& t, const Shape& s, Sol
     // A grid narrower than the chip streams through fewer CUs, each of which sustains about 1.25x
     // its share of the peak (fitted: 64-row workgroups at N = 11008 leave 84 CUs idle).
     const double cu_share = hbm_gbps(h) * 1e3 * kStreamEff / double(cus(h)) * 1.25;  // bytes per us
-    const double narrow_us = double(w.bytes) / useful / (double(std::min<int64_t>(grid, cus(h))) * cu_share);
+    const double narrow_us = double(w.bytes) / (double(std::min<int64_t>(grid, cus(h))) * cu_share);
     const double stream =
-        std::max(stream_us(h, double(w.bytes) / useful, grid, resident, inflight, false, 0.0, kQ8LatencyUs), narrow_us);
+        std::max(stream_us(h, double(w.bytes), grid, resident, inflight, false, 0.0, kQ8LatencyUs), narrow_us);
     const double cost = launch_us(h) + stream + issue_us + gen_us + act_us + rounds_us + hide_us;
     Cand c;
     c.plan.family = Family::Q8Gemm;

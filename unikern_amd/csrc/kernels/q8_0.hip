@@ -329,8 +329,8 @@ __global__ void __launch_bounds__(WAVES * 64)
 // nothing, so each wavefront owns one whole weight row and reduces it on the vector ALUs: the
 // row is K/32 * 34 contiguous bytes (4352 at K = 4096), copied into the wavefront's LDS area with
 // 1 KiB direct-to-LDS instructions (whole 128-byte lines except at the ends, where the tile
-// kernels copy 272-byte row segments), lane l takes block pairs l, l + 64, ... and a DPP
-// wavefront sum replaces the tile kernels' LDS fold and its barrier.
+// kernels copy 272-byte row segments), lane l takes block pair l, and a DPP wavefront sum replaces
+// the tile kernels' LDS fold and its barrier.
 // The activation row is copied into LDS once per workgroup (WAVES rows share it), 128 bytes per
 // block pair, with the eight 16-byte chunks of pair p rotated by p (slot s holds chunk
 // (s - p) mod 8): a lane reading chunk k of its pair reads slot (k + p) mod 8, so the 64 lanes'
@@ -338,11 +338,12 @@ __global__ void __launch_bounds__(WAVES * 64)
 // groups (the unrotated layout measured 5.45 against 5.12 us at N = K = 4096).
 // Per block: 16 v_dot2_f32_f16 of the quants (as binary16, exact, by the 1024-bias trick of
 // q4_to_f16) with the activations, f32 accumulation; the pair adds d_odd * s_odd + d_even * s_even
-// and a lane's pairs add in order; the wavefront sum is a fixed DPP tree (deterministic).
-// K: a multiple of 256 (16-byte aligned rows of whole block-pair quadruples), at most 4096 PL.
-// Rows past N copy row N - 1 (valid memory) and are never stored. FULL: K = 4096 PL exactly, every
-// count a compile-time constant (the general form's run-time copy counts and wait cost 5.49 against
-// 5.12 us at N = K = 4096).
+// and the wavefront sum is a fixed DPP tree (deterministic).
+// K: a multiple of 256 (16-byte aligned rows of whole block-pair quadruples), at most 4096 (one
+// pair per lane; with two, at K = 4608-8192, the 16-wavefront tile kernel measured faster at three
+// of four shapes). Rows past N copy row N - 1 (valid memory) and are never stored. FULL: K = 4096,
+// every count a compile-time constant (the general form's run-time copy counts and wait cost 5.49
+// against 5.12 us at N = K = 4096).
 // Four quants (one dword) -> binary16 -> s + q . x over four activations (two dwords).
 // The two f16 pairs enter __builtin_amdgcn_fdot2 as separate values: this compiler, given the
 // pairs packed into a two-dword vector (as q4_to_f16 returns them) and extracted again, fed the
@@ -388,12 +389,12 @@ __device__ __forceinline__ void q8_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int WAVES, int PL, bool FULL>
+template <int WAVES, bool FULL>
 __global__ void __launch_bounds__(WAVES * 64)
     q8_0_gemv_kernel(const _Float16* __restrict__ X, const uint8_t* __restrict__ Wq, float* __restrict__ Y, int N,
                      int K) {
   asm volatile("" ::"s"(X), "s"(Wq), "s"(Y), "s"(N), "s"(K));
-  constexpr int kMaxPairs = 64 * PL;
+  constexpr int kMaxPairs = 64;
   constexpr int kRowDw = 17 * kMaxPairs;                        // the longest row, in dwords
   constexpr int kInstMax = (kMaxPairs * 68 / 16 + 63) / 64;      // its 16-byte copy instructions
   static_assert(kInstMax <= 15, "the weight copies fit the explicit vmcnt waits");
@@ -433,30 +434,27 @@ __global__ void __launch_bounds__(WAVES * 64)
   q8_wait_vmcnt<0>();
 
   float y = 0.f;
+  const int p = lane;  // this lane's block pair
+  if (p < npairs) {
+    const uint32_t* pw = mine + 17 * p;
+    uint32_t dw[17];
 #pragma unroll
-  for (int j = 0; j < PL; ++j) {
-    const int p = lane + 64 * j;
-    if (p < npairs) {
-      const uint32_t* pw = mine + 17 * p;
-      uint32_t dw[17];
+    for (int d = 0; d < 17; ++d) dw[d] = pw[d];
+    const unsigned char* xl = xs + 128 * p;
+    u32x4 xv[8];
 #pragma unroll
-      for (int d = 0; d < 17; ++d) dw[d] = pw[d];
-      const unsigned char* xl = xs + 128 * p;
-      u32x4 xv[8];
+    for (int k = 0; k < 8; ++k) xv[k] = *reinterpret_cast<const u32x4*>(xl + 16 * ((k + p) & 7));
+    // Even block: quant dword k is bytes 2 + 4k .. 5 + 4k of the pair; odd block: dwords 9-16.
+    float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) xv[k] = *reinterpret_cast<const u32x4*>(xl + 16 * ((k + p) & 7));
-      // Even block: quant dword k is bytes 2 + 4k .. 5 + 4k of the pair; odd block: dwords 9-16.
-      float s0 = 0.f, s1 = 0.f;
+    for (int k = 0; k < 8; ++k)
+      s0 = q4_dot(__builtin_amdgcn_alignbyte(dw[k + 1], dw[k], 2), xv[k >> 1][(k & 1) * 2],
+                  xv[k >> 1][(k & 1) * 2 + 1], s0);
 #pragma unroll
-      for (int k = 0; k < 8; ++k)
-        s0 = q4_dot(__builtin_amdgcn_alignbyte(dw[k + 1], dw[k], 2), xv[k >> 1][(k & 1) * 2],
-                    xv[k >> 1][(k & 1) * 2 + 1], s0);
-#pragma unroll
-      for (int k = 0; k < 8; ++k)
-        s1 = q4_dot(dw[9 + k], xv[4 + (k >> 1)][(k & 1) * 2], xv[4 + (k >> 1)][(k & 1) * 2 + 1], s1);
-      const float d0 = half_bits_to_float(dw[0]), d1 = half_bits_to_float(dw[8] >> 16);
-      y += fmaf(d1, s1, d0 * s0);
-    }
+    for (int k = 0; k < 8; ++k)
+      s1 = q4_dot(dw[9 + k], xv[4 + (k >> 1)][(k & 1) * 2], xv[4 + (k >> 1)][(k & 1) * 2 + 1], s1);
+    const float d0 = half_bits_to_float(dw[0]), d1 = half_bits_to_float(dw[8] >> 16);
+    y = fmaf(d1, s1, d0 * s0);
   }
   y = wave_sum(y);
   if (lane == 0 && n < N) Y[n] = y;
@@ -467,14 +465,14 @@ __global__ void __launch_bounds__(WAVES * 64)
 namespace uk {
 
 namespace {
-template <int WAVES, int PL>
+template <int WAVES>
 hipError_t q8_gemv_go(const void* X, const void* Wq, float* Y, int64_t N, int64_t K, hipStream_t s) {
   const dim3 grid((unsigned)((N + WAVES - 1) / WAVES));
-  if (K == 4096 * PL)
-    hipLaunchKernelGGL((kern::q8_0_gemv_kernel<WAVES, PL, true>), grid, dim3(WAVES * 64), 0, s,
+  if (K == 4096)
+    hipLaunchKernelGGL((kern::q8_0_gemv_kernel<WAVES, true>), grid, dim3(WAVES * 64), 0, s,
                        static_cast<const _Float16*>(X), static_cast<const uint8_t*>(Wq), Y, (int)N, (int)K);
   else
-    hipLaunchKernelGGL((kern::q8_0_gemv_kernel<WAVES, PL, false>), grid, dim3(WAVES * 64), 0, s,
+    hipLaunchKernelGGL((kern::q8_0_gemv_kernel<WAVES, false>), grid, dim3(WAVES * 64), 0, s,
                        static_cast<const _Float16*>(X), static_cast<const uint8_t*>(Wq), Y, (int)N, (int)K);
   return hipGetLastError();
 }
@@ -539,11 +537,9 @@ hipError_t launch_q8_gemm(const Plan& p, const void* X, const void* Wq, float* Y
   if ((((uintptr_t)X) & 15) || (((uintptr_t)Wq) & 3) || (((uintptr_t)Y) & 3)) return hipErrorInvalidValue;
   const Q8Variant v = kQ8Variants[p.variant];
   if (v.gemv) {
-    // One activation row; rows of whole block-pair quadruples (16-byte aligned), at most 64 pairs
-    // per lane set.
-    if (M != 1 || K % 256 != 0 || K > 4096 * v.pairs || (((uintptr_t)Wq) & 15)) return hipErrorInvalidValue;
-    if (v.waves == 4 && v.pairs == 1) return q8_gemv_go<4, 1>(X, Wq, Y, N, K, s);
-    if (v.waves == 4 && v.pairs == 2) return q8_gemv_go<4, 2>(X, Wq, Y, N, K, s);
+    // One activation row; rows of whole block-pair quadruples (16-byte aligned), one pair per lane.
+    if (M != 1 || K % 256 != 0 || K > 4096 || (((uintptr_t)Wq) & 15)) return hipErrorInvalidValue;
+    if (v.waves == 4) return q8_gemv_go<4>(X, Wq, Y, N, K, s);
     return hipErrorInvalidValue;
   }
   // 16-byte copies: every wavefront segment (64 P elements of K) starts 16-byte aligned.

@@ -113,14 +113,13 @@ constexpr int kGemmGenericTile = 64;
 // round's copies in flight while the current round is computed. nt: 16-row weight tiles that
 // share each activation fragment.
 // gemv: the M = 1 kernel instead (one weight row per wavefront, vector-ALU dot products, `waves`
-// rows per workgroup sharing the activation row in LDS); `pairs` is then the number of block
-// pairs per lane it holds (K <= 4096 pairs).
+// rows per workgroup sharing the activation row in LDS, one block pair per lane: K <= 4096).
 struct Q8Variant {
   int waves, pairs, vec, db, nt, gemv;
 };
 constexpr Q8Variant kQ8Variants[] = {{16, 4, 4, 0, 1}, {16, 4, 1, 0, 1}, {8, 8, 4, 0, 1}, {8, 4, 1, 0, 1},
                                      {8, 4, 4, 1, 1},  {4, 4, 4, 1, 1},  {4, 8, 4, 1, 1}, {8, 4, 4, 0, 4},
-                                     {8, 4, 4, 0, 1},  {8, 4, 4, 0, 3},  {4, 1, 4, 0, 1, 1}, {4, 2, 4, 0, 1, 1}};
+                                     {8, 4, 4, 0, 1},  {8, 4, 4, 0, 3},  {4, 1, 4, 0, 1, 1}};
 constexpr int kNumQ8Variants = sizeof(kQ8Variants) / sizeof(kQ8Variants[0]);
 
 // Implicit-GEMM conv on f32 MFMA (v_mfma_f32_32x32x2f32). Wide kernel (tile_strips 0): a

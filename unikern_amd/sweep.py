@@ -7,7 +7,7 @@ the prediction beside the measurement. Run under rocprofv3, it attributes counte
 variant's kernel; `--summarize` turns a `--pmc GRBM_GUI_ACTIVE SQ_VALU_MFMA_BUSY_CYCLES
 SQ_BUSY_CU_CYCLES` run into a table of matrix-core busy fraction and shader clock per kernel.
 
-    python3 -m unikern_amd.sweep [gemm_f16] [conv] [gemm_f32] [q8_0] [q8_narrow] [rows] [offgrid] [--iters N]
+    python3 -m unikern_amd.sweep [gemm_f16] [conv] [gemm_f32] [q8_0] [q8_narrow] [q8_longk] [rows] [offgrid] [--iters N]
     python3 -m unikern_amd.sweep --summarize PMC_DIR
 
 Counter arithmetic (gfx950, 8 XCDs of 32 CUs, 4 SIMDs per CU): GRBM_GUI_ACTIVE is summed over
@@ -39,6 +39,10 @@ SHAPES = {
     # 8-way row split holds) and the down projection's long K: the Q8_0 ranking off its grid.
     "q8_narrow": [("gemm", [m, n, k], dict(dtype="q8_0", layout="TN"))
                   for n, k in ((512, 4096), (1376, 4096), (4096, 11008)) for m in (1, 16)],
+    # One activation row at K beyond the one-row-per-wavefront kernel's 4096 (the tile kernels'
+    # partial last rounds).
+    "q8_longk": [("gemm", [1, n, k], dict(dtype="q8_0", layout="TN"))
+                 for n, k in ((4096, 4608), (4096, 6144), (4096, 8192), (11008, 8192), (14336, 5120))],
     # Shapes none of the variant efficiencies was fitted at: the solver's ranking off its grid.
     "offgrid": [("gemm", [2048, 2048, 2048], dict(dtype="fp16", layout="TN")),
                 ("gemm", [8192, 4096, 4096], dict(dtype="fp16", layout="TN")),
@@ -58,6 +62,9 @@ def sweep(families, iters: int = 50, out=sys.stdout):
             d = uk.make_desc(op, dims, **kw)
             sol = uk.solve(d)
             print(f"{fam} {op} {dims}: solver pick {sol.key} (predicted {sol.predicted_us:.2f} us)", file=out, flush=True)
+            # One untimed run of the pick first: the first candidate timed after a change of shape
+            # read up to 1.8x its time at a 2.2 MB Q8_0 shape (and matched it when re-timed).
+            uk.run(d, iters=iters)
             for m in _CAND.finditer(sol.log):
                 key, family, variant, pred = m.group(1), int(m.group(2)), int(m.group(3)), float(m.group(4))
                 p = uk.Plan()
