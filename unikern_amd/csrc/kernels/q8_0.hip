@@ -340,8 +340,8 @@ __global__ void __launch_bounds__(WAVES * 64)
 // q4_to_f16) with the activations, f32 accumulation; the pair adds d_odd * s_odd + d_even * s_even
 // and the wavefront sum is a fixed DPP tree (deterministic).
 // K: a multiple of 256 (16-byte aligned rows of whole block-pair quadruples), at most 4096 (one
-// pair per lane; with two, at K = 4608-8192, the 16-wavefront tile kernel measured faster at three
-// of four shapes). Rows past N copy row N - 1 (valid memory) and are never stored. FULL: K = 4096,
+// pair per lane; with two, at K = 4608-8192, the 16-wavefront tile kernel measured faster at four
+// of five shapes). Rows past N copy row N - 1 (valid memory) and are never stored. FULL: K = 4096,
 // every count a compile-time constant (the general form's run-time copy counts and wait cost 5.49
 // against 5.12 us at N = K = 4096).
 // Four quants (one dword) -> binary16 -> s + q . x over four activations (two dwords).
