@@ -91,6 +91,16 @@ def test_run_q8_0_configs(gpu, M, N):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("M", [1, 16])
+def test_run_q8_0_exact_mode_bit_exact(gpu, M):
+    # Small-integer activations and power-of-two scales keep every partial sum exact in f32,
+    # so the MFMA tile kernel (M = 16) and the one-row kernel (M = 1) must match bit for bit.
+    r = gpu.run(gpu.make_desc("gemm", [M, 4096, 4096], dtype="q8_0", layout="TN"), exact=True, iters=5)
+    _ok(r)
+    assert r.err_metric == 0 and "bit_exact" in r.line
+
+
+@pytest.mark.gpu
 def test_run_conv_config(gpu):
     d = gpu.make_desc("conv", [56, 56, 64, 3, 3, 64], layout="NCHW", batch=8, pad=1, epilogue="channelscale")
     r = gpu.run(d, iters=20)

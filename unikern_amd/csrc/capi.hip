@@ -819,14 +819,26 @@ void make_inputs(const KmlTree& t, uint64_t seed, bool exact, RunData* rd) {
         HostTensor x;
         x.bytes.resize(size_t(s.M * s.K) * 2);
         std::vector<float> xf(size_t(s.M * s.K));
-        fill_normal(xf.data(), xf.size(), seed + kSeedQ8X, 0.f, 1.f);
-        for (size_t i = 0; i < xf.size(); ++i) x.as<uint16_t>()[i] = f32_to_f16(xf[i]);
-        std::vector<float> u(size_t(s.N * s.K));
-        fill_uniform(u.data(), u.size(), seed + kSeedQ8Q, 0.f, 1.f);
-        std::vector<int8_t> q(u.size());
-        for (size_t i = 0; i < u.size(); ++i) q[i] = int8_t(int(u[i] * 255.0f) - 127);
+        std::vector<int8_t> q(size_t(s.N * s.K));
         std::vector<float> df(size_t(s.N * nb));
-        fill_uniform(df.data(), df.size(), seed + kSeedQ8D, 1e-3f, 1e-2f);
+        // Exact mode: activations in {-2..2}, q a sawtooth over [-127, 127], scales 2^-4..2^-6.
+        // Every product is a multiple of 2^-6 below 2^4 in magnitude, so any partial sum in any
+        // order stays a multiple of 2^-6 below K * 2^4; for K <= 16384 that is under 2^24
+        // quanta, every sum is exact in f32 and the result must equal the binary64 reference
+        // rounded once, bit for bit.
+        const bool q8_exact = exact && s.K <= 16384;
+        if (q8_exact) {
+          for (size_t i = 0; i < xf.size(); ++i) xf[i] = float(int(i % 5) - 2);
+          for (size_t i = 0; i < q.size(); ++i) q[i] = int8_t(int(i % 255) - 127);
+          for (size_t i = 0; i < df.size(); ++i) df[i] = std::ldexp(1.0f, -4 - int(i % 3));
+        } else {
+          fill_normal(xf.data(), xf.size(), seed + kSeedQ8X, 0.f, 1.f);
+          std::vector<float> u(q.size());
+          fill_uniform(u.data(), u.size(), seed + kSeedQ8Q, 0.f, 1.f);
+          for (size_t i = 0; i < u.size(); ++i) q[i] = int8_t(int(u[i] * 255.0f) - 127);
+          fill_uniform(df.data(), df.size(), seed + kSeedQ8D, 1e-3f, 1e-2f);
+        }
+        for (size_t i = 0; i < xf.size(); ++i) x.as<uint16_t>()[i] = f32_to_f16(xf[i]);
         std::vector<uint16_t> dh(df.size());
         for (size_t i = 0; i < df.size(); ++i) dh[i] = f32_to_f16(df[i]);
         HostTensor w;
@@ -838,8 +850,8 @@ void make_inputs(const KmlTree& t, uint64_t seed, bool exact, RunData* rd) {
         rd->ref.resize(size_t(s.M * s.N));
         timed_ref(rd, s.N,
                   [&] { ref_q8_0(rd->ins[0].as<uint16_t>(), rd->ins[1].as<uint8_t>(), rd->ref.data(), s.M, s.N, s.K); });
-        rd->tol_kind = 2;
-        rd->tol = 1e-5;
+        rd->tol_kind = q8_exact ? 3 : 2;
+        rd->tol = q8_exact ? 0 : 1e-5;
         break;
       }
       const bool f16 = t.dtype == DType::F16;
