@@ -406,10 +406,15 @@ std::optional<Plan> solve_q8(const Hcs& h, const KmlTree& t, const Shape& s, Sol
     // Copy instructions: 16-byte copies issue a quarter of the dword ones.
     const double issue_us = double(rounds) * (v.vec == 4 ? 0.1 : 0.4);
     // Each generation of resident workgroups waits one load latency before its first round
-    // lands and folds its split-K partials after its last.
+    // lands and folds its split-K partials after its last. Only the first generation's wait is
+    // exposed whole: the CUs reach their later generations at different times, so a later one's
+    // wait overlaps the other CUs' streams and a quarter of it shows (fitted over the Q8_0 sweep
+    // of 20 shapes: any share from 0.1 to 0.3 gives the same picks; the whole wait for every
+    // generation took a tile kernel of three or four 16-row tiles per workgroup 8-18% slower than
+    // the 16-wavefront one at long-K single rows).
     const int64_t slots = int64_t(cus(h)) * resident;
     const int64_t generations = (grid + slots - 1) / slots;
-    const double gen_us = double(generations) * 0.25 * kMemLatencyUs;
+    const double gen_us = (1.0 + 0.25 * double(generations - 1)) * 0.25 * kMemLatencyUs;
     // Every workgroup reads its activation rows over all of K (from L2); the n-tiles of a
     // workgroup share each activation fragment: the busiest CU's activation bytes.
     const double act_cu = std::ceil(double(grid) / cus(h)) * double(std::min<int64_t>(s.M, 16)) * double(s.K) * 2.0;
