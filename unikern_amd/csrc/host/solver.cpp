@@ -196,7 +196,7 @@ std::optional<Plan> solve_rows(const Hcs& h, const KmlTree& t, const Shape& s, S
 }
 
 // ---------------------------------------------------------------------------------------
-constexpr double kGemmF32Eff = 0.65;  // gemm_f32_kernel's fraction of the f32 MFMA rate (calibrated at 1024^3)
+constexpr double kGemmF32Eff = 0.72;  // gemm_f32_kernel's fraction of the f32 MFMA rate (calibrated at 1024^3)
 
 std::optional<Plan> solve_gemm(const Hcs& h, const KmlTree& t, const Shape& s, SolveLog* log, std::string* err) {
   const double peak_tflops = t.dtype == DType::F16 ? (h.peak_f16_mfma_tflops > 0 ? h.peak_f16_mfma_tflops : h.flops_gflops * 1e-3)
@@ -298,7 +298,7 @@ std::optional<Plan> solve_gemm(const Hcs& h, const KmlTree& t, const Shape& s, S
       c.plan.threads = 512;
       c.plan.grid = tiles;
       c.plan.key = key;
-      c.plan.why = std::to_string(tiles) + " tiles of 64x64, LDS-staged k-tiles of 64 split over two wavefronts per SIMD";
+      c.plan.why = std::to_string(tiles) + " tiles of 64x64, k-tiles of 64 copied into LDS one ahead, split over two wavefronts per SIMD";
       c.cost = launch_us(h) +
                per_cu * 2.0 * 64 * 64 * double(s.K) / (cu_flops_per_us * kGemmF32Eff * mfma_clock_scale(h)) + 1.0;
       cs.push_back(c);

@@ -49,8 +49,10 @@
 //
 // gemm_f32_kernel — f32 C = A . B (B stored [K][N] or [N][K]) on v_mfma_f32_32x32x2f32 for
 //   M, N, K multiples of 64: a 64x64 tile per workgroup of eight wavefronts. Each k-tile of 64
-//   is staged in LDS (float4 loads and stores, rows padded to 68 floats so the fragment reads
-//   of eight lanes hit distinct bank groups) and split between two wavefronts per SIMD: waves
+//   moves into LDS by direct-to-LDS copies issued one tile ahead (rows of 256 bytes, 16-byte
+//   chunks rotated by row so the fragment reads of eight lanes hit distinct bank groups; the
+//   register-staged form with float4 stores into padded rows took 24.2-24.3 us at 1024^3 NN
+//   against 21.9-22.2, same bits) and split between two wavefronts per SIMD: waves
 //   0-3 multiply its first 32 k, waves 4-7 its last 32, each a 32x32 quarter of the tile, so one
 //   wavefront's LDS reads and waits overlap the other's MFMAs. A lane's float4 of A (and of B
 //   when B is [N][K]) feeds four MFMAs: MFMA (q, e) pairs k = 8q + e on lanes 0-31 with
@@ -1320,8 +1322,6 @@ __global__ void __launch_bounds__(512, 1)
 // ---------------------------------------------------------------------------------------
 // f32 GEMM, 64x64x64 tiles, eight wavefronts (two k halves x 2x2 quarters).
 // ---------------------------------------------------------------------------------------
-constexpr int kF32Pitch = 68;  // floats per staged row (64 + 4 padding)
-
 template <bool BT>
 __global__ void __launch_bounds__(512)
     gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N,
@@ -1329,8 +1329,8 @@ __global__ void __launch_bounds__(512)
   // All arguments in scalar registers before anything else (one wait for their loads, not one per
   // argument between the computations that need them).
   asm volatile("" ::"s"(A), "s"(B), "s"(C), "s"(M), "s"(N), "s"(K), "s"(tiles_m), "s"(tiles_n), "s"(gridDim.x));
-  constexpr int kBuf = 2 * 64 * kF32Pitch;  // A and B of one k-tile
-  __shared__ __attribute__((aligned(16))) float lds[2 * kBuf];
+  constexpr int kOp = 64 * 64;  // floats of one operand's k-tile: 64 rows of 256 bytes
+  __shared__ __attribute__((aligned(16))) float lds[2 * 2 * kOp];  // two slots of (A, B)
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kh = w >> 2, wm = (w >> 1) & 1, wn = w & 1;
@@ -1348,47 +1348,47 @@ __global__ void __launch_bounds__(512)
   const int gm = (tiles_m - first_m) < kGroupM ? (tiles_m - first_m) : kGroupM;
   const int in_group = lin - group * per_group;
   const int m0 = (first_m + in_group % gm) * 64, n0 = (in_group / gm) * 64;
-  // Staging: thread -> rows (tid >> 4) + 32u (u < 2), float4 column tid & 15 of a 64-float row:
-  // A rows are m, B rows are n (B [N][K]) or k (B [K][N]).
-  const int srow = tid >> 4, scol = (tid & 15) * 4;
-  const float* a_src = A + (int64_t)(m0 + srow) * K + scol;
-  const float* b_src = BT ? B + (int64_t)(n0 + srow) * K + scol : B + (int64_t)srow * N + n0 + scol;
-  const int64_t a_step32 = (int64_t)32 * K;                 // 32 rows of A
-  const int64_t b_step32 = BT ? (int64_t)32 * K : (int64_t)32 * N;
-  f32x4 ra[2], rb[2];
-  auto load = [&](int t) __attribute__((always_inline)) {
-    const int k0 = t * 64;
+  // Copies: an operand's k-tile is 16 instructions of four 256-byte rows; wavefront w issues
+  // instructions 2w and 2w + 1, and lane l fills 16-byte slot l & 15 of row 4 (2w + i) + (l >> 4).
+  // Rows read down a column of chunks (A's m rows; B's n rows when B is [N][K]) hold chunk c of
+  // row r in slot c ^ (r & 7); B's k rows ([K][N]) are read along the row and keep chunk order.
+  const float* a_src[2];
+  const float* b_src[2];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      ra[u] = *reinterpret_cast<const f32x4*>(a_src + u * a_step32 + k0);
-      rb[u] = BT ? *reinterpret_cast<const f32x4*>(b_src + u * b_step32 + k0)
-                 : *reinterpret_cast<const f32x4*>(b_src + u * b_step32 + (int64_t)k0 * N);
-    }
-  };
-  auto store = [&](int b) __attribute__((always_inline)) {
-    float* as = lds + b * kBuf;
-    float* bs = as + 64 * kF32Pitch;
+  for (int i = 0; i < 2; ++i) {
+    const int r = 4 * (2 * w + i) + (lane >> 4), sl = lane & 15;
+    a_src[i] = A + (int64_t)(m0 + r) * K + 4 * (sl ^ (r & 7));
+    b_src[i] = BT ? B + (int64_t)(n0 + r) * K + 4 * (sl ^ (r & 7)) : B + (int64_t)r * N + n0 + 4 * sl;
+  }
+  auto copy = [&](int t, int slot) __attribute__((always_inline)) {
+    float* as = lds + slot * 2 * kOp;
+    float* bs = as + kOp;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      *reinterpret_cast<f32x4*>(as + (srow + 32 * u) * kF32Pitch + scol) = ra[u];
-      *reinterpret_cast<f32x4*>(bs + (srow + 32 * u) * kF32Pitch + scol) = rb[u];
-    }
+    for (int i = 0; i < 2; ++i)
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(a_src[i] + t * 64),
+                                       (lds_void*)(as + (2 * w + i) * 256), 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      __builtin_amdgcn_global_load_lds(
+          reinterpret_cast<const uint32_t*>(BT ? b_src[i] + t * 64 : b_src[i] + (int64_t)t * 64 * N),
+          (lds_void*)(bs + (2 * w + i) * 256), 16, 0, 0);
   };
   const int fi = lane & 31, fh = lane >> 5;
-  const int kb = 32 * kh + 4 * fh;  // this lane's k offset within the tile (plus 8q + e)
+  const int ra = wm * 32 + fi, rb = wn * 32 + fi;
   f32x16 acc = f32x16{};
-  auto multiply = [&](int b) __attribute__((always_inline)) {
-    const float* as = lds + b * kBuf;
-    const float* bs = as + 64 * kF32Pitch;
+  auto multiply = [&](int slot) __attribute__((always_inline)) {
+    const float* as = lds + slot * 2 * kOp;
+    const float* bs = as + kOp;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const f32x4 av = *reinterpret_cast<const f32x4*>(as + (wm * 32 + fi) * kF32Pitch + kb + 8 * q);
+      const int c = 8 * kh + fh + 2 * q;  // the 16-byte chunk of k = 32 kh + 4 fh + 8 q
+      const f32x4 av = *reinterpret_cast<const f32x4*>(as + ra * 64 + 4 * (c ^ (ra & 7)));
       f32x4 bv;
       if constexpr (BT) {
-        bv = *reinterpret_cast<const f32x4*>(bs + (wn * 32 + fi) * kF32Pitch + kb + 8 * q);
+        bv = *reinterpret_cast<const f32x4*>(bs + rb * 64 + 4 * (c ^ (rb & 7)));
       } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) bv[e] = bs[(kb + 8 * q + e) * kF32Pitch + wn * 32 + fi];
+        for (int e = 0; e < 4; ++e) bv[e] = bs[(4 * c + e) * 64 + rb];
       }
       acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, bv.x, acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, bv.y, acc, 0, 0, 0);
@@ -1396,23 +1396,26 @@ __global__ void __launch_bounds__(512)
       acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, bv.w, acc, 0, 0, 0);
     }
   };
+  // Tile t + 1's copies go into the slot tile t - 1 left (every wavefront passed the barrier
+  // after reading it) before tile t's MFMAs, and each wavefront waits for its own copies before
+  // the barrier that publishes the tile. The barrier carries no memory fence (that would also
+  // wait for the copies in flight); this wavefront's LDS reads are complete by then, since the
+  // MFMAs consumed them.
   const int KT = K / 64;
-  load(0);
-  store(0);
-  __syncthreads();
+  copy(0, 0);
+  wait_vmcnt<0>();
+  barrier_nofence();
   for (int t = 0; t < KT; ++t) {
-    // The next tile's loads are in flight during this tile's MFMAs (the last pass repeats the
-    // last tile: unbranched, so the loads are not sunk behind the MFMAs).
-    load(t + 1 < KT ? t + 1 : t);
+    if (t + 1 < KT) copy(t + 1, (t + 1) & 1);
     __builtin_amdgcn_sched_barrier(0);
     multiply(t & 1);
     __builtin_amdgcn_sched_barrier(0);
-    store((t + 1) & 1);  // its last readers (tile t - 1) passed the previous barrier
-    __syncthreads();
+    wait_vmcnt<0>();
+    barrier_nofence();
   }
   // D[i][j]: lane -> column j = lane & 31, rows i = 8 (r / 4) + 4 (lane >> 5) + r % 4. The k
   // halves add in LDS (first half + second half) and the first half stores.
-  float* red = lds;  // every wavefront passed the last barrier: the ring is free
+  float* red = lds;  // every wavefront passed the last barrier and every copy landed
   const int q4 = w & 3;
   if (kh == 1) {
 #pragma unroll
@@ -1420,7 +1423,7 @@ __global__ void __launch_bounds__(512)
   }
   __syncthreads();
   if (kh == 1) return;
-  const int j = n0 + wn * 32 + fi;
+  const int j = n0 + rb;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int i = m0 + wm * 32 + (r >> 2) * 8 + fh * 4 + (r & 3);
