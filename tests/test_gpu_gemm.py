@@ -119,11 +119,11 @@ def test_f32_generic(gpu, M, N, K, layout):
 
 
 @pytest.mark.parametrize("vi", [0, 1])
-@pytest.mark.parametrize("M,N,K", [(64, 64, 64), (128, 192, 320), (256, 128, 512)])
+@pytest.mark.parametrize("M,N,K", [(64, 64, 64), (128, 192, 320), (256, 128, 512), (1024, 1536, 704)])
 @pytest.mark.parametrize("layout", ["NT", "TN"])
 def test_f32_variants(gpu, vi, M, N, K, layout):
     # variant 0: bounds-checked generic kernel; 1: the LDS-tiled kernel (one and several tiles,
-    # one and an odd number of k-tiles); tolerance and exact mode
+    # one and an odd number of k-tiles, more tiles than CUs); tolerance and exact mode
     p = gpu.Plan()
     p.family, p.variant = 6, vi
     A = O.uniform(M * K, 5 + M + vi, -1.0, 1.0).reshape(M, K)
