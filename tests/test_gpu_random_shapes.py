@@ -46,6 +46,17 @@ def test_f32_gemm_random(gpu, layout, M, N, K):
     assert frob(C, O.gemm_f32(A, B, layout == "TN")) <= 1e-5
 
 
+@pytest.mark.parametrize("layout", ["NT", "TN"])
+@pytest.mark.parametrize("M,N,K", [(64 * m, 64 * n, 64 * k) for m, n, k in draws(16, 6, (1, 24), (1, 24), (1, 24))])
+def test_f32_gemm_random_tiled(gpu, layout, M, N, K):
+    # 64-multiples: the solver routes these to the direct-to-LDS tiled kernel.
+    assert gpu.solve(gpu.make_desc("gemm", [M, N, K], dtype="fp32", layout=layout)).key == "gemm_f32:64x64x64,w8"
+    A = O.uniform(M * K, 7400 + M, -1.0, 1.0).reshape(M, K)
+    B = O.uniform(N * K, 7500 + N, -1.0, 1.0).reshape((N, K) if layout == "TN" else (K, N))
+    C = gemm_gpu(gpu, A, B, "fp32", layout)
+    assert frob(C, O.gemm_f32(A, B, layout == "TN")) <= 1e-5
+
+
 @pytest.mark.parametrize("N,C,H,W,Oc,Kh,Kw,pad,stride",
                          [(n, c, h, w, oc, k, k, p, s)
                           for (n, c, h, w, oc, k, p, s) in draws(13, 8, (1, 3), (1, 24), (3, 40), (3, 40), (1, 70),
