@@ -116,6 +116,15 @@ def test_run_commits_then_hits(gpu, tmp_path, sample):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("sample", ["kml_q8_0_m1_n4096.json", "kml_q8_0_m16_n11008.json"])
+def test_run_exact_mode_q8_0_is_bit_exact(gpu, tmp_path, sample):
+    rc, out, err = cli(gpu, "run", "--hcs", "builtin", "--kml", SAMPLES / sample, "--iters", "5", "--exact",
+                       cwd=tmp_path)
+    assert rc == 0, out + err
+    assert "verify=PASS" in out and " gate=bit_exact_mismatches err=0.000000e+00 " in out, out
+
+
+@pytest.mark.gpu
 def test_run_exact_mode_and_calibrate(gpu, tmp_path):
     kml = SAMPLES / "kml_softmax_4096.json"
     rc, out, err = cli(gpu, "run", "--hcs", SAMPLES / "hcs_mi355x.json", "--kml", kml, "--ledger", "c.jsonl",
